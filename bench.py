@@ -1,0 +1,303 @@
+#!/usr/bin/env python3
+"""Benchmark of the int4 MatMulNBits library on one MI355X.
+
+Workload (the headline metric "int4 MatMulNBits GB/s at M=1 and TFLOP/s at
+M=512, Phi-3-mini shapes"):
+
+* step = one Phi-3-mini decode step at M=1: every quantized projection of 32
+  layers (qkv 3072->9216, o_proj 3072->3072, gate_up 3072->16384,
+  down 8192->3072) plus lm_head 3072->32064, block size 32, no zero-point
+  tensor (implicit 8), run back to back.  About 2.1 GB of packed int4 weights
+  and fp16 scales stay resident in HBM; each projection has its own fp16
+  activation (N(0,1)) and fp16 output buffer.  Weights are random (seeded);
+  there is no checkpoint.  The step is captured once in a HIP graph and
+  replayed; inputs are resident before the timed region starts.
+* value = algorithmic bytes per step / wall time per step, in GB/s.
+* prefill: the same 129 projections at M = 512 (and a sweep over
+  M = 16, 128, 2048), reported as TFLOP/s (2*M*N*K flops).
+* roofline: per-launch HIP-event timing of the dominant kernel (the M=1
+  kernel) and of the M=512 kernel, against 8 TB/s HBM and 2.5 PFLOP/s fp16.
+* cpu_baseline: the oracle's restatement of the reference's Java CPU path
+  (8-lane FMA block dot, one thread per core) on a bounded sample of the
+  same decode step.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "win-directml-java_amd"), os.path.join(ROOT, "oracle")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+BLOCK = 32
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-sweep", action="store_true")
+    return p.parse_args()
+
+
+class Launcher:
+    """Direct C-ABI calls for a fixed list of (weight, x, y) triples."""
+
+    def __init__(self, ctx, weights, xs, ys, M, stream):
+        import mnb_hip
+        self.lib = mnb_hip.load()
+        self.calls = []
+        for w, x, y in zip(weights, xs, ys):
+            self.calls.append((ctx.handle, w.handle, M, ctypes.c_void_p(x.data_ptr()), mnb_hip.MNB_F16,
+                               x.numel(), ctypes.c_void_p(y.data_ptr()), mnb_hip.MNB_F16, y.numel(), 0,
+                               ctypes.c_void_p(stream.cuda_stream)))
+
+    def run(self, idx=None):
+        import mnb_hip
+        f = self.lib.mnb_matmul
+        for a in (self.calls if idx is None else [self.calls[i] for i in idx]):
+            rc = f(*a)
+            if rc != 0:
+                raise mnb_hip.MnbError(rc, mnb_hip.last_error())
+
+
+def time_graph(torch, graph, stream, steps, warmup):
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            graph.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        ev0.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    gpu = ev0.elapsed_time(ev1) / 1e3 / steps
+    return wall, gpu
+
+
+def per_launch_times(torch, launcher, stream, reps=3):
+    """Kernel duration of every launch, from a HIP event pair around it.  The
+    stream is first held by a GPU sleep so that all launches are queued
+    before the first one starts (no host gaps inside a bracket)."""
+    n = len(launcher.calls)
+    durs = np.zeros((reps, n))
+    for r in range(reps):
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(int(40e6))
+            for i in range(n):
+                evs[i][0].record(stream)
+                launcher.run([i])
+                evs[i][1].record(stream)
+        torch.cuda.synchronize()
+        durs[r] = [a.elapsed_time(b) / 1e3 for a, b in evs]
+    return durs.min(axis=0)
+
+
+def capture(torch, launcher, stream):
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        launcher.run()          # eager run first (validates every call)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=stream):
+        launcher.run()
+    torch.cuda.synchronize()
+    return g
+
+
+def copy_bandwidth(torch, stream):
+    n = 1 << 30
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(10):
+            b.copy_(a)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) / 1e3 / 10
+    del a, b
+    return 2 * n / t / 1e9
+
+
+def cpu_baseline(host, projs, seconds):
+    """Oracle restatement of the reference CPU path on a bounded sample."""
+    import mnb_oracle as orc
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    orc.build()
+    rng = np.random.default_rng(99)
+    done_bytes = 0
+    done = 0
+    t_total = 0.0
+    while t_total < seconds and done < len(projs):
+        (name, layer, K, N), t = projs[done], host[done]
+        s32 = orc.fp16_bits_to_fp32(t.scales_f16.view(np.uint16))
+        z = np.full((N * t.kb + 1) // 2, 0x88, np.uint8)
+        x = rng.standard_normal(K).astype(np.float16).astype(np.float32)
+        y = np.zeros(N, np.float32)
+        t0 = time.perf_counter()
+        orc.matvec(t.q, s32, z, N, K, BLOCK, x, y, lanes=8, threads=threads)
+        t_total += time.perf_counter() - t0
+        done_bytes += t.algorithmic_bytes(1)
+        done += 1
+    return {"value": round(done_bytes / t_total / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": "first %d of the %d decode-step projections at M=1 (%.2f GB), fp32 activations, "
+                      "8-lane FMA block dot, %d threads, %.1f s" % (done, len(projs), done_bytes / 1e9, threads,
+                                                                     t_total)}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py measures one GPU; this build has no multi-GPU path (requested --gpus %d)" % args.gpus,
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import mnb_hip
+    from mnb_hip import synth
+
+    ctx = mnb_hip.Context(0)
+    info = ctx.info()
+    log("device %s %s, %d CUs" % (info.name.decode(), info.arch.decode(), info.compute_units))
+    stream = torch.cuda.Stream()
+
+    projs = synth.phi3_decode_step()
+    host, weights = [], []
+    t0 = time.perf_counter()
+    for i, (name, layer, K, N) in enumerate(projs):
+        t = synth.make_weight(10_000 + i, N, K, BLOCK)
+        host.append(t)
+        weights.append(mnb_hip.Weight(ctx, N, K, BLOCK, t.q, t.scales_f16))
+    log("uploaded %d weights (%.2f GB resident) in %.1f s" % (
+        len(weights), sum(w.device_bytes for w in weights) / 1e9, time.perf_counter() - t0))
+    bytes_step = sum(t.algorithmic_bytes(1) for t in host)
+
+    # ---------------- decode step, M = 1 ----------------
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    xs = [torch.randn(K, device="cuda", generator=gen).half() for (_, _, K, _) in projs]
+    ys = [torch.empty(N, device="cuda", dtype=torch.float16) for (_, _, _, N) in projs]
+    dec = Launcher(ctx, weights, xs, ys, 1, stream)
+    g_dec = capture(torch, dec, stream)
+    wall, gpu = time_graph(torch, g_dec, stream, args.steps, args.warmup)
+    value = bytes_step / wall / 1e9
+    log("decode step: %.1f us wall, %.1f us gpu, %.1f GB/s" % (wall * 1e6, gpu * 1e6, value))
+    d1 = per_launch_times(torch, dec, stream)
+    achieved_gbs = bytes_step / d1.sum() / 1e9
+    per_shape = {}
+    for (name, layer, K, N), t, d in zip(projs, host, d1):
+        e = per_shape.setdefault(name, {"K": K, "N": N, "bytes": t.algorithmic_bytes(1), "us": []})
+        e["us"].append(d * 1e6)
+    for name, e in per_shape.items():
+        us = float(np.mean(e.pop("us")))
+        e["avg_us"] = round(us, 3)
+        e["gbs"] = round(e["bytes"] / us / 1e3, 1)
+    log("per-launch: " + json.dumps(per_shape))
+    del g_dec
+
+    # ---------------- prefill, M = 512 (+ sweep) ----------------
+    def prefill(M):
+        xs_m, ys_m = {}, []
+        for (_, _, K, N) in projs:
+            if K not in xs_m:
+                xs_m[K] = torch.randn(M, K, device="cuda", generator=gen).half()
+        xs_l = [xs_m[K] for (_, _, K, _) in projs]
+        ybuf = {}
+        for (_, _, K, N) in projs:
+            if N not in ybuf:
+                ybuf[N] = torch.empty(M, N, device="cuda", dtype=torch.float16)
+            ys_m.append(ybuf[N])
+        la = Launcher(ctx, weights, xs_l, ys_m, M, stream)
+        g = capture(torch, la, stream)
+        steps = max(3, args.steps // 4) if M >= 512 else args.steps
+        wall_m, gpu_m = time_graph(torch, g, stream, steps, 2)
+        flops = sum(2.0 * M * N * K for (_, _, K, N) in projs)
+        del g
+        return la, flops, wall_m, gpu_m
+
+    la512, flops512, wall512, gpu512 = prefill(512)
+    tflops512 = flops512 / wall512 / 1e12
+    d512 = per_launch_times(torch, la512, stream, reps=2)
+    kernel_tflops512 = flops512 / d512.sum() / 1e12
+    log("prefill M=512: %.1f us wall, %.1f TFLOP/s (kernel-time %.1f TFLOP/s)" % (
+        wall512 * 1e6, tflops512, kernel_tflops512))
+    del la512
+    sweep = {}
+    if not args.no_sweep:
+        for M in (16, 128, 2048):
+            _, fl, w_m, _ = prefill(M)
+            sweep[str(M)] = round(fl / w_m / 1e12, 2)
+            log("prefill M=%d: %.1f TFLOP/s" % (M, sweep[str(M)]))
+            torch.cuda.empty_cache()
+
+    copy_gbs = copy_bandwidth(torch, stream)
+    log("device copy bandwidth: %.0f GB/s" % copy_gbs)
+
+    for w in weights:
+        w.close()
+    ctx.close()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(host, projs, args.cpu_seconds)
+        log("cpu baseline: %s" % json.dumps(cpu))
+
+    result = {
+        "metric": "int4 MatMulNBits GB/s at M=1 (Phi-3-mini decode step)",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded random int4 weights, fp16 scales in [0.005,0.02], fp16 N(0,1) activations)",
+        "config": {"workload": "phi3-mini int4 decode step: 32 x {qkv 3072->9216, o 3072->3072, "
+                               "gate_up 3072->16384, down 8192->3072} + lm_head 3072->32064, M=1, bs=32, "
+                               "implicit zero point 8, HIP graph of 129 launches",
+                   "M": 1, "block_size": BLOCK, "projections": len(projs), "bytes_per_step": bytes_step},
+        "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "mnb::gemv_kernel (M=1)", "per_shape": per_shape},
+        "prefill_m512": {"tflops": round(tflops512, 2), "ms_per_step": round(wall512 * 1e3, 4),
+                         "flops_per_step": flops512, "frac_fp16_peak": round(tflops512 / FP16_PEAK_TFLOPS, 4),
+                         "roofline": {"bound": "mfma", "achieved": round(kernel_tflops512, 2),
+                                      "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                      "frac": round(kernel_tflops512 / FP16_PEAK_TFLOPS, 4),
+                                      "kernel": "mnb::gemm_kernel (M=512)"},
+                         "sweep_tflops": sweep},
+        "device_copy_gbs": round(copy_gbs, 1),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,187 @@
+/*
+ * mnb.h -- C ABI of libmnb_hip.so, the MI355X (gfx950) int4 MatMulNBits library.
+ *
+ * One weight object holds one MatMulNBits weight triplet (packed uint4 nibbles,
+ * per-block scales, optional packed uint4 zero points) resident in HBM.  The
+ * library owns every device buffer it creates; weights are uploaded once.
+ *
+ * Each entry point names the reference interface it replaces.  Paths are
+ * relative to the reference repository root:
+ *   MNK = directml-windows-bindings/src/main/java/com/aresstack/windirectml/windows/MatMulNBitsKernel.java
+ *   P3W = directml-inference/src/main/java/com/aresstack/windirectml/inference/phi3/Phi3Weights.java
+ *   Q2W = directml-inference/src/main/java/com/aresstack/windirectml/inference/qwen/Qwen2Weights.java
+ *   QLK = directml-windows-bindings/src/main/java/com/aresstack/windirectml/runtime/kernels/QuantizedLinearKernel.java
+ *
+ * Conventions
+ *   - Every function returns an int32_t status (MNB_OK = 0).  On failure a
+ *     message is available from mnb_last_error() on the calling thread.
+ *   - Status codes map onto the reference's exceptions:
+ *       MNB_ERR_INVALID_ARGUMENT -> IllegalArgumentException
+ *       MNB_ERR_INVALID_STATE    -> IllegalStateException ("Kernel not prepared")
+ *       everything else          -> RuntimeException("MatMulNBitsKernel.<op> failed")
+ *   - A weight object is not thread-safe for concurrent calls that use host
+ *     memory (they share the context's staging buffers), the same as one
+ *     reference kernel instance (MNK:77-81).  Calls with device pointers on
+ *     distinct streams may run concurrently.
+ *   - Pointers: by default x/y/out are DEVICE pointers and the call is
+ *     asynchronous on `stream` (a hipStream_t; NULL = the context's stream).
+ *     With MNB_HOST_MEMORY they are host pointers, the call copies through
+ *     device staging buffers and returns when the result is in host memory
+ *     (the reference's float[] contract, MNK:1847-1914).
+ */
+#ifndef MNB_H
+#define MNB_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MNB_ABI_VERSION 1
+
+/* status codes */
+#define MNB_OK 0
+#define MNB_ERR_INVALID_ARGUMENT 1
+#define MNB_ERR_INVALID_STATE 2
+#define MNB_ERR_OUT_OF_MEMORY 3
+#define MNB_ERR_DEVICE 4
+#define MNB_ERR_NO_DEVICE 5
+#define MNB_ERR_UNSUPPORTED 6
+
+/* element types */
+#define MNB_F32 0
+#define MNB_F16 1
+
+/* zero-point layouts accepted by mnb_weight_create */
+#define MNB_ZP_NONE 0       /* no tensor: implicit zero point 8 (P3W:593-598, Q2W:1107-1112) */
+#define MNB_ZP_FLAT 1       /* flat nibble stream, nibble n*kb+blk, low nibble first, (N*kb+1)/2 bytes (MNK:258-262) */
+#define MNB_ZP_ROW_PADDED 2 /* ONNX MatMulNBits layout [N, ceil(kb/2)] (Q2W:1055-1075) */
+
+/* flags */
+#define MNB_HOST_MEMORY 0x1u /* x/y/out are host pointers; the call is synchronous */
+#define MNB_ACCUMULATE 0x2u  /* y += x W^T (QuantizedWeight.matvec/matmul, P3W:123-192) instead of y = x W^T */
+
+typedef struct mnb_context mnb_context;
+typedef struct mnb_weight mnb_weight;
+
+typedef struct mnb_device_info {
+    char name[64];
+    char arch[64];
+    int32_t compute_units;
+    int32_t clock_khz;
+    int32_t memory_clock_khz;
+    int32_t memory_bus_width;
+    int64_t total_memory;
+    int32_t l2_bytes;
+    int32_t lds_bytes_per_block;
+    int32_t wavefront_size;
+    int32_t device;
+} mnb_device_info;
+
+/* Library version (MNB_ABI_VERSION).  No reference counterpart. */
+int32_t mnb_version(void);
+
+/* Message of the last failed call on this thread ("" if none).  Replaces the
+ * exception messages of MNK:1849-1850, 1909-1913 and 966-969. */
+const char *mnb_last_error(void);
+
+/* Open the library on HIP device `device`.  Replaces WindowsBindings.init
+ * plus the per-kernel command allocator/queue/fence set-up (MNK:1168-1247,
+ * prepareExecInfraInt4).  Fails with MNB_ERR_NO_DEVICE when no gfx950 device
+ * is present. */
+int32_t mnb_context_create(int32_t device, mnb_context **out);
+
+/* Release the context's stream and staging buffers.  Weights created on it
+ * must be destroyed first (MNB_ERR_INVALID_STATE otherwise). */
+int32_t mnb_context_destroy(mnb_context *ctx);
+
+/* Device properties used for the roofline (peak clocks, CU count, memory). */
+int32_t mnb_context_info(const mnb_context *ctx, mnb_device_info *out);
+
+/* Upload one weight triplet once.  Replaces the INT4 constructor
+ * `new MatMulNBitsKernel(wb, N, K, byte[] qWeight, float[] scales,
+ * byte[] zeroPoints, int blockSize)` (MNK:940-970 -> prepareInt4Gpu
+ * MNK:1168-1247) and QLK:25-31's weight/scales/zeros operands.
+ *
+ *   N, K        output and input features.  K may be the true K; the packed
+ *               tensors always hold kb = ceil(K/block_size) full blocks per
+ *               row.  Passing the reference's K (= kb*block_size) is the
+ *               same call as the reference.
+ *   block_size  power of two in [16, 4096]
+ *   bits        must be 4
+ *   q           uint8 [N, kb, block_size/2], two nibbles per byte, low first; q_bytes >= N*kb*block_size/2
+ *   scales      [N, kb] of scale_type (MNB_F16 bit patterns or MNB_F32); scale_count >= N*kb.
+ *               F32 scales are kept exactly (device copy is fp16 when every
+ *               value is exactly representable, else fp32).
+ *   zero_points layout per zp_layout; NULL with MNB_ZP_NONE
+ *   flags       0 (host pointers for all tensors)
+ */
+int32_t mnb_weight_create(mnb_context *ctx, int32_t N, int32_t K, int32_t block_size, int32_t bits,
+                          const uint8_t *q, int64_t q_bytes, const void *scales, int32_t scale_type,
+                          int64_t scale_count, const uint8_t *zero_points, int64_t zp_bytes, int32_t zp_layout,
+                          uint32_t flags, mnb_weight **out);
+
+/* Free the weight's device buffers.  Replaces MatMulNBitsKernel.close()
+ * (MNK:2740-2800).  NULL is accepted. */
+int32_t mnb_weight_destroy(mnb_weight *w);
+
+/* N, K (as passed at creation) and block size.  Replaces getN()/getK()
+ * (MNK:2803-2812). */
+int32_t mnb_weight_shape(const mnb_weight *w, int32_t *N, int32_t *K, int32_t *block_size);
+
+/* Bytes of HBM the weight occupies (packed nibbles, scales, zero points). */
+int64_t mnb_weight_device_bytes(const mnb_weight *w);
+
+/* y[M, N] = x[M, K] W^T  (or += with MNB_ACCUMULATE).
+ * Replaces matvec(float[] x, float[] out) (M = 1, overwrite, MNK:1847-1914),
+ * matmulBatch(float[] xBatch, float[] outBatch, int M) (overwrite,
+ * MNK:2145-2263), the resident variants (MNK:1687-1832, 2276-2358) when
+ * called with device pointers, QuantizedWeight.matvec/matmul (accumulate,
+ * P3W:123-192, Q2W:80-147) with MNB_ACCUMULATE, and QLK:25-31 dispatch.
+ *
+ *   x_type, y_type  MNB_F16 or MNB_F32; x is [M, K] row-major, y is [M, N]
+ *   x_elems         number of elements the caller's x holds; M == 1 requires
+ *                   x_elems == K ("Input length L != K=K"), M > 1 requires >= M*K
+ *   y_elems         elements in y; must be >= M*N
+ *   M               any M >= 1 (no 256-row chunking is needed)
+ * Arithmetic: products of fp16 operands accumulated in fp32.  The output is
+ * within 1e-3*sqrt(K)*max|x|*max|w| of the reference's fp32 CPU path.
+ */
+int32_t mnb_matmul(mnb_context *ctx, const mnb_weight *w, int32_t M, const void *x, int32_t x_type,
+                   int64_t x_elems, void *y, int32_t y_type, int64_t y_elems, uint32_t flags, void *stream);
+
+/* Dequantize to out[N, K] (K as passed at creation), w = (q - zp) * scale
+ * computed in fp32 and written as fp32, or rounded to nearest-even fp16.
+ * Replaces MatMulNBitsKernel.dequantizeInt4 (MNK:2674-2705); the fp32 output
+ * is bit-identical to it. */
+int32_t mnb_dequantize(mnb_context *ctx, const mnb_weight *w, void *out, int32_t out_type, int64_t out_elems,
+                       uint32_t flags, void *stream);
+
+/* Always true for a created weight.  Replaces supportsBatch() (MNK:2128). */
+int32_t mnb_supports_batch(const mnb_weight *w);
+
+/* Largest M one mnb_matmul call accepts.  Replaces maxBatchRows()
+ * (MNK:2361, which is 256 there). */
+int32_t mnb_max_batch_rows(void);
+
+/* Device buffers for resident activations (WarpGpuBuffer in the reference,
+ * used by MNK:1687-1832). */
+int32_t mnb_device_alloc(mnb_context *ctx, int64_t bytes, void **out);
+int32_t mnb_device_free(mnb_context *ctx, void *ptr);
+
+#define MNB_COPY_H2D 0
+#define MNB_COPY_D2H 1
+#define MNB_COPY_D2D 2
+/* Synchronous copy on the context's stream. */
+int32_t mnb_memcpy(mnb_context *ctx, void *dst, const void *src, int64_t bytes, int32_t kind);
+
+/* Wait for all work on the context's stream.  Replaces the fence wait
+ * (MNK:1894-1901). */
+int32_t mnb_synchronize(mnb_context *ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MNB_H */

@@ -1,0 +1,374 @@
+"""GPU parity of libmnb_hip against the oracle, through the C ABI.
+
+Bars (stated per test):
+* dequantize: bit-exact to the reference's dequantizeInt4 (fp32), and fp16
+  output = round-to-nearest-even of that fp32 value.
+* matmul: |y - y_oracle| <= 1e-3 * sqrt(K) * max|x| * max|w| (K = true K),
+  plus one fp16 ulp of |y_oracle| when the output is fp16.
+* full-size shapes: the oracle on sampled output rows, and properties that
+  hold bit-for-bit (power-of-two scaling, row independence, M-tiling).
+"""
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import mnb_hip
+from mnb_hip import synth
+import mnb_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    orc.build()
+    c = mnb_hip.Context(0)
+    i = c.info()
+    say("device:", i.name.decode(), i.arch.decode(), "CUs", i.compute_units)
+    yield c
+    c.close()
+
+
+THREADS = min(16, len(os.sched_getaffinity(0)))
+
+
+def fp16_ulp(v):
+    a = np.abs(np.asarray(v, np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
+    return 2.0 ** (e - 10)
+
+
+def oracle_inputs(t: synth.QuantTensor, rows=None):
+    """Reference-form tensors: fp32 scales (loader widening), flat zero points
+    (runtime layout; 0x88 when absent), optionally restricted to `rows`."""
+    kb, bs = t.kb, t.bs
+    q = t.q.reshape(t.N, kb * bs // 2)
+    s = orc.fp16_bits_to_fp32(t.scales_f16.view(np.uint16)).reshape(t.N, kb)
+    if t.zp_row_padded is not None:
+        zrp = t.zp_row_padded
+    else:
+        zrp = np.full((t.N, (kb + 1) // 2), 0x88, np.uint8)
+    if rows is not None:
+        q, s, zrp = q[rows], s[rows], zrp[rows]
+    n = q.shape[0]
+    z = synth.zp_row_padded_to_flat(zrp, n, kb)
+    return q.reshape(-1), s.reshape(-1), z, n
+
+
+def oracle_matmul(t: synth.QuantTensor, x16: np.ndarray, rows=None):
+    q, s, z, n = oracle_inputs(t, rows)
+    kpad = t.kb * t.bs
+    M = x16.shape[0]
+    x = np.zeros((M, kpad), np.float32)
+    x[:, : t.K] = x16.astype(np.float32)
+    y = orc.matmul(q, s, z, n, kpad, t.bs, x, threads=THREADS)
+    wmax = float(np.max(np.abs(orc.dequantize(q, s, z, n, kpad, t.bs)))) if n * kpad <= 64 << 20 else None
+    return y, wmax
+
+
+def max_abs_w(t: synth.QuantTensor) -> float:
+    """max|w| = max over blocks of scale * max|q - zp| (exact, no dequant needed)."""
+    s = t.scales_f16.astype(np.float32).reshape(t.N, t.kb)
+    return float(np.max(np.abs(s)) * 15.0) if t.zp_row_padded is not None else float(np.max(np.abs(s)) * 8.0)
+
+
+def assert_parity(y, y_ref, x16, t, wmax=None, fp16_out=False, label=""):
+    K = t.K
+    wm = wmax if wmax is not None else max_abs_w(t)
+    tol = 1e-3 * np.sqrt(K) * float(np.max(np.abs(x16.astype(np.float32)))) * wm
+    allowed = tol + (fp16_ulp(y_ref) if fp16_out else 0.0)
+    err = np.abs(y.astype(np.float64) - y_ref.astype(np.float64))
+    worst = float(np.max(err - allowed))
+    say("parity %s: max|err|=%.3e tol=%.3e" % (label, float(np.max(err)), tol))
+    assert np.all(np.isfinite(y)), label
+    assert worst <= 0.0, "%s: max|err| %.3e exceeds bound %.3e" % (label, float(np.max(err)), tol)
+
+
+def upload(ctx, t: synth.QuantTensor, as_f32_scales=False):
+    s = t.scales_f16.astype(np.float32) if as_f32_scales else t.scales_f16
+    if t.zp_row_padded is not None:
+        return mnb_hip.Weight(ctx, t.N, t.K, t.bs, t.q, s, t.zp_row_padded, mnb_hip.MNB_ZP_ROW_PADDED)
+    return mnb_hip.Weight(ctx, t.N, t.K, t.bs, t.q, s)
+
+
+# ------------------------------------------------------------ dequant -----
+
+def test_dequant_bit_exact_on_golden_fixtures(ctx, golden_dir):
+    d = np.load(os.path.join(golden_dir, "dequant_exact.npz"), allow_pickle=False)
+    names = sorted({k.split("__")[0] for k in d.files})
+    done = 0
+    for n in names:
+        N, K, bs = (int(v) for v in d[n + "__shape"])
+        if bs < 16:
+            continue    # MatMulNBits block sizes start at 16
+        say("dequant golden", n)
+        w_exp = d[n + "__w"]
+        variants = [d[n + "__scales"]]
+        if d[n + "__scales_f16"].size:
+            variants.append(d[n + "__scales_f16"].view(np.float16))
+        for s in variants:
+            w = mnb_hip.Weight(ctx, N, K, bs, d[n + "__q"], s, d[n + "__zp"], mnb_hip.MNB_ZP_FLAT)
+            got = w.dequantize(np.float32)
+            assert np.array_equal(got.view(np.uint32), w_exp.view(np.uint32)), n
+            got16 = w.dequantize(np.float16)
+            assert np.array_equal(got16.view(np.uint16), w_exp.astype(np.float16).view(np.uint16)), n
+            w.close()
+            done += 1
+    assert done >= 8
+
+
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("K,N", synth.SMOL_SHAPES)
+def test_dequant_config4_bit_exact(ctx, bs, K, N):
+    say("dequant config4", K, N, bs)
+    t = synth.make_weight(1000 + bs + K, N, K, bs, with_zp=True)
+    q, s, z, n = oracle_inputs(t)
+    kpad = t.kb * bs
+    ref = orc.dequantize(q, s, z, n, kpad, bs)[:, :K]
+    w = upload(ctx, t)
+    got = w.dequantize(np.float32)
+    assert np.array_equal(got.view(np.uint32), np.ascontiguousarray(ref).view(np.uint32))
+    got16 = w.dequantize(np.float16)
+    assert np.array_equal(got16.view(np.uint16), ref.astype(np.float16).view(np.uint16))
+    w.close()
+
+
+def test_dequant_reference_loader_subnormal_scales(ctx):
+    """fp16 subnormal scales widened by the reference loader (m * 2^-150) and
+    passed as fp32 must dequantize bit-exactly like the reference."""
+    rng = np.random.default_rng(9)
+    N, K, bs = 32, 256, 32
+    q = rng.integers(0, 256, N * K // 2, dtype=np.uint8)
+    bits = rng.integers(1, 0x400, N * K // bs).astype(np.uint16)          # subnormal fp16 patterns
+    bits[::3] = rng.integers(0x0400, 0x7C00, bits[::3].size).astype(np.uint16)  # and normals
+    s_ref = orc.fp16_bits_to_fp32(bits)
+    z = orc.zp_pack_unpacked_u8(rng.integers(0, 16, N * K // bs), N, K // bs)
+    ref = orc.dequantize(q, s_ref, z, N, K, bs)
+    w = mnb_hip.Weight(ctx, N, K, bs, q, s_ref, z, mnb_hip.MNB_ZP_FLAT)
+    assert np.array_equal(w.dequantize(np.float32).view(np.uint32), ref.view(np.uint32))
+    w.close()
+
+
+# ------------------------------------------------------------- matmul -----
+
+def test_closed_form_kats(ctx, golden_dir):
+    import json
+    kat = json.load(open(os.path.join(golden_dir, "kat_closed_form.json")))
+    for c in kat["matvec"]:
+        say("kat", c["name"])
+        N, K = c["N"], 128
+        q = np.full(N * K // 2, (c["nibble"] & 0xF) * 0x11, np.uint8)
+        s = np.full(N, c["scale"], np.float32)
+        z = np.full((N + 1) // 2, (c["zp"] & 0xF) * 0x11, np.uint8)
+        k = mnb_hip.MatMulNBitsKernel(ctx, N, K, q, s, z, 128)
+        qm = mnb_hip.QuantizedWeightMatrix(k)
+        y = np.array(c["y_init"], np.float32)
+        qm.matvec(np.full(K, c["x"], np.float32), y)
+        assert np.allclose(y, c["expected"], atol=c["atol"], rtol=0), c["name"]
+        k.close()
+
+
+def test_config0_decode_gemv(ctx):
+    """M=1, K=3072, N=9216, bs=32, implicit zero point 8 (Phi-3 fused QKV)."""
+    t = synth.make_weight(0, 9216, 3072, 32)
+    x16 = synth.make_x(1, 1, 3072)
+    y_ref, wmax = oracle_matmul(t, x16)
+    w = upload(ctx, t)
+    for out_dt in (np.float16, np.float32):
+        y = w.matmul(x16, out_dtype=out_dt)
+        assert_parity(y, y_ref, x16, t, wmax, out_dt == np.float16, "cfg0 out=%s" % np.dtype(out_dt).name)
+    # the Java float[] contract: fp32 in, fp32 out
+    y = w.matmul(x16.astype(np.float32), out_dtype=np.float32)
+    assert_parity(y, y_ref, x16, t, wmax, False, "cfg0 f32->f32")
+    w.close()
+
+
+@pytest.mark.parametrize("M", [1, 7, 33])
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("K,N", synth.SMOL_SHAPES)
+def test_config4_asymmetric_tails(ctx, M, bs, K, N):
+    say("config4", M, bs, K, N)
+    t = synth.make_weight(2000 + M + bs + K, N, K, bs, with_zp=True)
+    x16 = synth.make_x(3000 + M, M, K)
+    y_ref, wmax = oracle_matmul(t, x16)
+    w = upload(ctx, t)
+    y = w.matmul(x16, out_dtype=np.float16)
+    assert_parity(y, y_ref, x16, t, wmax, True, "cfg4 M=%d bs=%d K=%d N=%d" % (M, bs, K, N))
+    w.close()
+
+
+@pytest.mark.parametrize("bs", [16, 256])
+def test_block_sizes_16_and_256(ctx, bs):
+    t = synth.make_weight(77 + bs, 200, 1024, bs, with_zp=True)
+    for M in (1, 5, 40):
+        x16 = synth.make_x(78 + M, M, 1024)
+        y_ref, wmax = oracle_matmul(t, x16)
+        w = upload(ctx, t)
+        assert_parity(w.matmul(x16), y_ref, x16, t, wmax, False, "bs=%d M=%d" % (bs, M))
+        w.close()
+
+
+@pytest.mark.parametrize("M", [1, 64])
+def test_config3_qwen_shapes(ctx, M):
+    for li, (name, K, N) in enumerate(synth.QWEN_LAYER + [synth.QWEN_LM_HEAD]):
+        say("config3", name, M)
+        t = synth.make_weight(4000 + li, N, K, 32)
+        x16 = synth.make_x(5000 + li + M, M, K)
+        rows = None
+        if N * M > 2_000_000:
+            rows = np.random.default_rng(li).choice(N, 2048, replace=False)
+            rows.sort()
+        y_ref, _ = oracle_matmul(t, x16, rows)
+        w = upload(ctx, t)
+        y = w.matmul(x16, out_dtype=np.float16)
+        ys = y if rows is None else y[:, rows] if y.ndim == 2 else y[rows]
+        assert_parity(ys, y_ref.reshape(ys.shape), x16, t, None, True, "cfg3 %s M=%d" % (name, M))
+        w.close()
+
+
+@pytest.mark.parametrize("M", [16, 128, 512, 2048])
+def test_config2_phi3_prefill_sampled_rows(ctx, M):
+    for li, (name, K, N) in enumerate(synth.PHI3_LAYER):
+        say("config2", name, M)
+        t = synth.make_weight(6000 + li, N, K, 32)
+        x16 = synth.make_x(7000 + li + M, M, K)
+        nrow = max(64, min(N, 16_000_000 // (M * K) * 4))
+        rows = np.sort(np.random.default_rng(M + li).choice(N, min(N, nrow), replace=False))
+        y_ref, _ = oracle_matmul(t, x16, rows)
+        w = upload(ctx, t)
+        y = w.matmul(x16, out_dtype=np.float16)
+        assert_parity(y[:, rows], y_ref, x16, t, None, True, "cfg2 %s M=%d" % (name, M))
+        w.close()
+
+
+# ------------------------------------------------ bitwise properties ------
+
+def test_rows_are_independent_in_skinny_kernel(ctx):
+    t = synth.make_weight(11, 3072, 3072, 32)
+    w = upload(ctx, t)
+    x16 = synth.make_x(12, 16, 3072)
+    y16 = w.matmul(x16)
+    for m in (0, 5, 15):
+        y1 = w.matmul(x16[m])
+        assert np.array_equal(y1.view(np.uint32), y16[m].view(np.uint32)), m
+    w.close()
+
+
+def test_gemm_tiling_invariance_and_pow2_scaling(ctx):
+    t = synth.make_weight(13, 3072, 3072, 32)
+    w = upload(ctx, t)
+    x16 = synth.make_x(14, 512, 3072)
+    y = w.matmul(x16)
+    y_part = w.matmul(np.ascontiguousarray(x16[128:256]))
+    assert np.array_equal(y[128:256].view(np.uint32), y_part.view(np.uint32))
+    y2 = w.matmul((x16.astype(np.float32) * 2).astype(np.float16))
+    assert np.array_equal(y2.view(np.uint32), (y * 2).view(np.uint32))
+    x1 = synth.make_x(15, 1, 3072)
+    g1 = w.matmul(x1[0])
+    g2 = w.matmul((x1[0].astype(np.float32) * 4).astype(np.float16))
+    assert np.array_equal(g2.view(np.uint32), (g1 * 4).view(np.uint32))
+    w.close()
+
+
+def test_accumulate_and_dtypes_and_zp_layouts(ctx):
+    t = synth.make_weight(21, 1536, 576, 64, with_zp=True)
+    w_rp = upload(ctx, t)
+    q, s, z, n = oracle_inputs(t)
+    w_flat = mnb_hip.Weight(ctx, t.N, t.K, t.bs, t.q, t.scales_f16, z, mnb_hip.MNB_ZP_FLAT)
+    for M in (1, 33):
+        x16 = synth.make_x(22 + M, M, 576)
+        a = w_rp.matmul(x16)
+        b = w_flat.matmul(x16)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        c = w_rp.matmul(x16.astype(np.float32))        # fp32 activations are rounded to fp16 first
+        assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
+        y0 = np.random.default_rng(M).standard_normal(a.shape).astype(np.float32)
+        acc = w_rp.matmul(x16, y=y0.copy(), accumulate=True)
+        assert np.array_equal(acc.view(np.uint32), (y0 + a).view(np.uint32))
+    w_rp.close()
+    w_flat.close()
+
+
+def test_fp32_scales_not_fp16_exact(ctx):
+    """Scales from the tied-lm_head quantizer are arbitrary fp32 values."""
+    rng = np.random.default_rng(31)
+    rows, cols, bs = 300, 896, 128
+    dense = rng.standard_normal((rows, cols)).astype(np.float32) * 0.05
+    q, s, z = orc.quantize_rows_u4(dense, rows, cols, bs)
+    w = mnb_hip.Weight(ctx, rows, cols, bs, q, s, z, mnb_hip.MNB_ZP_FLAT)
+    ref_w = orc.dequantize(q, s, z, rows, cols, bs)
+    assert np.array_equal(w.dequantize(np.float32).view(np.uint32), ref_w.view(np.uint32))
+    for M in (1, 64):
+        x16 = synth.make_x(32 + M, M, cols)
+        y_ref = orc.matmul(q, s, z, rows, cols, bs, x16.astype(np.float32), threads=THREADS)
+        tol = 1e-3 * np.sqrt(cols) * float(np.max(np.abs(x16.astype(np.float32)))) * float(np.max(np.abs(ref_w)))
+        err = float(np.max(np.abs(w.matmul(x16) - y_ref)))
+        say("fp32 scales M=%d max|err|=%.3e tol=%.3e" % (M, err, tol))
+        assert err <= tol
+    w.close()
+
+
+def test_device_pointers_match_host_path(ctx):
+    import torch
+    t = synth.make_weight(41, 9216, 3072, 32)
+    w = upload(ctx, t)
+    for M in (1, 64):
+        x16 = synth.make_x(42 + M, M, 3072)
+        host = w.matmul(x16, out_dtype=np.float16)
+        st = torch.cuda.Stream()
+        with torch.cuda.stream(st):
+            xd = torch.from_numpy(x16).cuda()
+            yd = torch.empty((M, t.N), dtype=torch.float16, device="cuda")
+            w.matmul(xd, yd, stream=st.cuda_stream)
+        torch.cuda.synchronize()
+        assert np.array_equal(yd.cpu().numpy().view(np.uint16), host.view(np.uint16))
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        wd = torch.empty((t.N, t.K), dtype=torch.float16, device="cuda")
+        w.dequantize(out=wd, stream=st.cuda_stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(wd.cpu().numpy().view(np.uint16), w.dequantize(np.float16).view(np.uint16))
+    w.close()
+
+
+# ---------------------------------------------------------- contract ------
+
+def test_cpp_mirror_contract():
+    """The C++ MatMulNBitsKernel mirror runs the reference's matvec KATs."""
+    assert os.path.exists(mnb_hip.CONTRACT_TEST_PATH), "contract test not built"
+    r = subprocess.run([mnb_hip.CONTRACT_TEST_PATH], capture_output=True, text=True, timeout=120)
+    say(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
+def test_error_paths(ctx):
+    t = synth.make_weight(51, 64, 256, 32)
+    k = mnb_hip.MatMulNBitsKernel(ctx, 64, 256, t.q, t.scales_f16.astype(np.float32), None, 32)
+    with pytest.raises(mnb_hip.IllegalArgumentException, match="Input length 255 != K=256"):
+        k.matvec(np.zeros(255, np.float32))
+    with pytest.raises(mnb_hip.IllegalArgumentException):
+        k.matmulBatch(np.zeros(256 * 2, np.float32), np.zeros(64, np.float32), 2)
+    with pytest.raises(mnb_hip.IllegalArgumentException):
+        mnb_hip.Weight(ctx, 64, 256, 48, t.q, t.scales_f16)      # block size not a power of two
+    with pytest.raises(mnb_hip.IllegalArgumentException):
+        mnb_hip.Weight(ctx, 64, 256, 32, t.q[:100], t.scales_f16)
+    k.close()
+    with pytest.raises(mnb_hip.IllegalStateException, match="Kernel not prepared"):
+        k.matvec(np.zeros(256, np.float32))
+    os.environ["MNB_FAULT_INJECT"] = "alloc"
+    try:
+        with pytest.raises(mnb_hip.MnbError) as ei:
+            mnb_hip.Weight(ctx, 64, 256, 32, t.q, t.scales_f16)
+        assert ei.value.code == mnb_hip.MNB_ERR_OUT_OF_MEMORY
+    finally:
+        del os.environ["MNB_FAULT_INJECT"]
+    w = mnb_hip.Weight(ctx, 64, 256, 32, t.q, t.scales_f16)     # recovers after the injected failure
+    w.close()

@@ -1,0 +1,519 @@
+// mnb_api.cpp -- the C ABI of libmnb_hip.so (declared in include/mnb.h).
+//
+// Host half of the reference's MatMulNBitsKernel
+// (directml-windows-bindings/src/main/java/com/aresstack/windirectml/windows/
+// MatMulNBitsKernel.java): argument validation with the reference's messages,
+// one-time weight residency (prepareInt4Gpu, :1168-1247), the host-array
+// call path (matvec :1847-1914, matmulBatch :2145-2263) and the
+// device-resident path.  The D3D12 command lists, fences and upload heaps
+// of the reference are replaced by one HIP stream per context.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <limits>
+#include <string>
+#include <vector>
+
+#include "mnb_internal.h"
+
+using mnb::WeightGeom;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int32_t fail(int32_t code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int32_t ok() { return MNB_OK; }
+
+int32_t hip_fail(hipError_t e, const char *op) {
+    int32_t code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? MNB_ERR_OUT_OF_MEMORY
+                                                                              : MNB_ERR_DEVICE;
+    return fail(code, "MatMulNBitsKernel.%s failed: %s (%s)", op, hipGetErrorString(e), hipGetErrorName(e));
+}
+
+// Fault injection for host-side error-path tests: MNB_FAULT_INJECT=alloc makes
+// every device allocation of the library fail as out-of-memory.
+bool inject_alloc_failure() {
+    const char *v = getenv("MNB_FAULT_INJECT");
+    return v && strcmp(v, "alloc") == 0;
+}
+
+hipError_t dev_alloc(void **p, size_t bytes) {
+    *p = nullptr;
+    if (inject_alloc_failure()) return hipErrorOutOfMemory;
+    if (bytes == 0) bytes = 16;
+    return hipMalloc(p, bytes);
+}
+
+// grow-only staging buffer
+hipError_t ensure(void **buf, size_t *cap, size_t bytes) {
+    if (*cap >= bytes && *buf) return hipSuccess;
+    if (*buf) {
+        hipError_t e = hipFree(*buf);
+        *buf = nullptr;
+        *cap = 0;
+        if (e != hipSuccess) return e;
+    }
+    size_t want = bytes < 4096 ? 4096 : bytes;
+    hipError_t e = dev_alloc(buf, want);
+    if (e == hipSuccess) *cap = want;
+    return e;
+}
+
+// IEEE binary32 -> binary16 bits, round to nearest even.
+uint16_t f32_to_f16_bits(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t a = x & 0x7FFFFFFFu;
+    if (a >= 0x7F800000u) return (uint16_t)(sign | (a == 0x7F800000u ? 0x7C00u : 0x7E00u | ((a >> 13) & 0x3FFu)));
+    const int e = (int)(a >> 23) - 127;
+    const uint32_t mant = a & 0x7FFFFFu;
+    if (e > 15) return (uint16_t)(sign | 0x7C00u);
+    if (e >= -14) {
+        uint32_t h = ((uint32_t)(e + 15) << 10) | (mant >> 13);
+        const uint32_t rem = mant & 0x1FFFu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+        return (uint16_t)(sign | h);
+    }
+    if (e < -25) return (uint16_t)sign;
+    const uint32_t full = mant | 0x800000u;
+    const int shift = (-14 - e) + 13;
+    uint32_t h = full >> shift;
+    const uint32_t rem = full & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (h & 1u))) ++h;
+    return (uint16_t)(sign | h);
+}
+
+// IEEE binary16 bits -> binary32 (exact).
+float f16_bits_to_f32(uint16_t h) {
+    const uint32_t s = (uint32_t)(h >> 15) << 31;
+    const uint32_t e = (h >> 10) & 0x1Fu;
+    uint32_t m = h & 0x3FFu;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = s;
+        } else {   // normalise the subnormal
+            int ee = -1;
+            do { ++ee; m <<= 1; } while ((m & 0x400u) == 0);
+            bits = s | ((uint32_t)(127 - 15 - ee) << 23) | ((m & 0x3FFu) << 13);
+        }
+    } else if (e == 31) {
+        bits = s | 0x7F800000u | (m << 13);
+    } else {
+        bits = s | ((e - 15 + 127) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+size_t dtype_size(int32_t t) { return t == MNB_F32 ? 4 : 2; }
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) (void)hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+int32_t mnb_version(void) { return MNB_ABI_VERSION; }
+
+const char *mnb_last_error(void) { return g_last_error.c_str(); }
+
+int32_t mnb_context_create(int32_t device, mnb_context **out) {
+    if (!out) return fail(MNB_ERR_INVALID_ARGUMENT, "out must not be null");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0)
+        return fail(MNB_ERR_NO_DEVICE, "no HIP device available (%s)", e != hipSuccess ? hipGetErrorString(e) : "0 devices");
+    if (device < 0 || device >= count)
+        return fail(MNB_ERR_INVALID_ARGUMENT, "device %d out of range [0, %d)", device, count);
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return hip_fail(e, "init");
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(MNB_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950 (MI355X)", device,
+                    prop.gcnArchName);
+    DeviceGuard guard(device);
+    mnb_context *c = new mnb_context();
+    c->device = device;
+    c->cu_count = prop.multiProcessorCount;
+    e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete c;
+        return hip_fail(e, "init");
+    }
+    mnb_device_info &i = c->info;
+    snprintf(i.name, sizeof i.name, "%s", prop.name);
+    snprintf(i.arch, sizeof i.arch, "%s", prop.gcnArchName);
+    i.compute_units = prop.multiProcessorCount;
+    i.clock_khz = prop.clockRate;
+    i.memory_clock_khz = prop.memoryClockRate;
+    i.memory_bus_width = prop.memoryBusWidth;
+    i.total_memory = (int64_t)prop.totalGlobalMem;
+    i.l2_bytes = prop.l2CacheSize;
+    i.lds_bytes_per_block = (int32_t)prop.sharedMemPerBlock;
+    i.wavefront_size = prop.warpSize;
+    i.device = device;
+    *out = c;
+    return ok();
+}
+
+int32_t mnb_context_destroy(mnb_context *ctx) {
+    if (!ctx) return ok();
+    if (ctx->live_weights > 0)
+        return fail(MNB_ERR_INVALID_STATE, "context still owns %lld weight(s); destroy them first",
+                    (long long)ctx->live_weights);
+    DeviceGuard guard(ctx->device);
+    hipError_t first = hipSuccess;
+    auto note = [&](hipError_t e) { if (first == hipSuccess && e != hipSuccess) first = e; };
+    note(hipStreamSynchronize(ctx->stream));
+    if (ctx->stage_raw) note(hipFree(ctx->stage_raw));
+    if (ctx->stage_x) note(hipFree(ctx->stage_x));
+    if (ctx->stage_y) note(hipFree(ctx->stage_y));
+    note(hipStreamDestroy(ctx->stream));
+    delete ctx;
+    if (first != hipSuccess) return hip_fail(first, "close");
+    return ok();
+}
+
+int32_t mnb_context_info(const mnb_context *ctx, mnb_device_info *out) {
+    if (!ctx || !out) return fail(MNB_ERR_INVALID_ARGUMENT, "context and out must not be null");
+    *out = ctx->info;
+    return ok();
+}
+
+int32_t mnb_weight_create(mnb_context *ctx, int32_t N, int32_t K, int32_t block_size, int32_t bits, const uint8_t *q,
+                          int64_t q_bytes, const void *scales, int32_t scale_type, int64_t scale_count,
+                          const uint8_t *zero_points, int64_t zp_bytes, int32_t zp_layout, uint32_t flags,
+                          mnb_weight **out) {
+    if (!out) return fail(MNB_ERR_INVALID_ARGUMENT, "out must not be null");
+    *out = nullptr;
+    if (!ctx) return fail(MNB_ERR_INVALID_STATE, "Kernel not prepared: no context");
+    if (bits != 4) return fail(MNB_ERR_UNSUPPORTED, "bits=%d: only 4-bit MatMulNBits is supported", bits);
+    if (N < 1 || K < 1) return fail(MNB_ERR_INVALID_ARGUMENT, "N=%d and K=%d must be positive", N, K);
+    if (!is_pow2(block_size) || block_size < 16 || block_size > 4096)
+        return fail(MNB_ERR_INVALID_ARGUMENT, "block_size=%d must be a power of two in [16, 4096]", block_size);
+    if (flags != 0) return fail(MNB_ERR_INVALID_ARGUMENT, "unknown flags 0x%x", flags);
+    if (!q || !scales) return fail(MNB_ERR_INVALID_ARGUMENT, "qWeight and scales must not be null");
+    if (scale_type != MNB_F16 && scale_type != MNB_F32)
+        return fail(MNB_ERR_INVALID_ARGUMENT, "scale_type=%d must be MNB_F16 or MNB_F32", scale_type);
+    WeightGeom g = mnb::make_geom(N, K, block_size);
+    const int64_t blocks = (int64_t)N * g.kb;
+    const int64_t need_q = (int64_t)N * g.Kpad / 2;
+    if (q_bytes < need_q)
+        return fail(MNB_ERR_INVALID_ARGUMENT, "qWeight too short: %lld bytes < N*kb*blockSize/2 = %lld",
+                    (long long)q_bytes, (long long)need_q);
+    if (scale_count < blocks)
+        return fail(MNB_ERR_INVALID_ARGUMENT, "scales too short: %lld < N*kb = %lld", (long long)scale_count,
+                    (long long)blocks);
+
+    // zero points -> flat nibble stream (Qwen2Weights.java:1023-1112)
+    std::vector<uint8_t> zp_flat;
+    if (zp_layout == MNB_ZP_NONE) {
+        if (zero_points) return fail(MNB_ERR_INVALID_ARGUMENT, "zero_points given with MNB_ZP_NONE");
+    } else if (zp_layout == MNB_ZP_FLAT || zp_layout == MNB_ZP_ROW_PADDED) {
+        if (!zero_points) return fail(MNB_ERR_INVALID_ARGUMENT, "zero_points must not be null for this layout");
+        const int64_t flat_bytes = (blocks + 1) / 2;
+        zp_flat.assign((size_t)flat_bytes, 0);
+        if (zp_layout == MNB_ZP_FLAT) {
+            if (zp_bytes < flat_bytes)
+                return fail(MNB_ERR_INVALID_ARGUMENT, "zero points truncated: %lld bytes, expected %lld",
+                            (long long)zp_bytes, (long long)flat_bytes);
+            memcpy(zp_flat.data(), zero_points, (size_t)flat_bytes);
+        } else {
+            const int64_t row_bytes = (g.kb + 1) / 2;
+            if (zp_bytes < (int64_t)N * row_bytes)
+                return fail(MNB_ERR_INVALID_ARGUMENT, "zero points truncated: %lld bytes, expected %lld",
+                            (long long)zp_bytes, (long long)N * row_bytes);
+            for (int64_t n = 0; n < N; ++n)
+                for (int64_t b = 0; b < g.kb; ++b) {
+                    const int64_t src = n * row_bytes * 2 + b;
+                    const uint8_t v = (zero_points[src / 2] >> (4 * (src & 1))) & 0xF;
+                    const int64_t dst = n * g.kb + b;
+                    zp_flat[(size_t)(dst / 2)] |= (uint8_t)(v << (4 * (dst & 1)));
+                }
+        }
+        g.has_zp = 1;
+    } else {
+        return fail(MNB_ERR_INVALID_ARGUMENT, "zp_layout=%d is not a known layout", zp_layout);
+    }
+
+    // scales: keep fp16 unless an fp32 value is not exactly representable
+    std::vector<uint16_t> s16;
+    const void *s_src = scales;
+    size_t s_elem = 2;
+    if (scale_type == MNB_F32) {
+        const float *sf = (const float *)scales;
+        bool exact = true;
+        s16.resize((size_t)blocks);
+        for (int64_t i = 0; i < blocks; ++i) {
+            const uint16_t h = f32_to_f16_bits(sf[i]);
+            const float back = f16_bits_to_f32(h);
+            if (memcmp(&back, &sf[i], 4) != 0) { exact = false; break; }
+            s16[(size_t)i] = h;
+        }
+        if (exact) {
+            s_src = s16.data();
+        } else {
+            g.scale_f32 = 1;
+            s_elem = 4;
+            s16.clear();
+        }
+    }
+
+    DeviceGuard guard(ctx->device);
+    mnb_weight *w = new mnb_weight();
+    w->ctx = ctx;
+    w->g = g;
+    const size_t tiles = (size_t)g.NT * g.ST;
+    const size_t q_t_bytes = tiles * mnb::kTileBytes;
+    const size_t s_t_bytes = tiles * mnb::kTileRows * g.SPS * s_elem;
+    const size_t z_t_bytes = g.has_zp ? tiles * mnb::kTileRows * g.ZB : 0;
+    void *q_nat = nullptr, *s_nat = nullptr, *z_nat = nullptr;
+    hipError_t e = hipSuccess;
+    auto cleanup_tmp = [&]() {
+        if (q_nat) (void)hipFree(q_nat);
+        if (s_nat) (void)hipFree(s_nat);
+        if (z_nat) (void)hipFree(z_nat);
+    };
+    auto cleanup_all = [&]() {
+        cleanup_tmp();
+        if (w->q_t) (void)hipFree(w->q_t);
+        if (w->s_t) (void)hipFree(w->s_t);
+        if (w->zp_t) (void)hipFree(w->zp_t);
+        delete w;
+    };
+    if ((e = dev_alloc(&w->q_t, q_t_bytes)) != hipSuccess ||
+        (e = dev_alloc(&w->s_t, s_t_bytes)) != hipSuccess ||
+        (g.has_zp && (e = dev_alloc(&w->zp_t, z_t_bytes)) != hipSuccess) ||
+        (e = dev_alloc(&q_nat, (size_t)need_q)) != hipSuccess ||
+        (e = dev_alloc(&s_nat, (size_t)blocks * s_elem)) != hipSuccess ||
+        (g.has_zp && (e = dev_alloc(&z_nat, zp_flat.size())) != hipSuccess)) {
+        cleanup_all();
+        return hip_fail(e, "prepare");
+    }
+    if ((e = hipMemcpyAsync(q_nat, q, (size_t)need_q, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess ||
+        (e = hipMemcpyAsync(s_nat, s_src, (size_t)blocks * s_elem, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess ||
+        (g.has_zp && (e = hipMemcpyAsync(z_nat, zp_flat.data(), zp_flat.size(), hipMemcpyHostToDevice, ctx->stream)) != hipSuccess) ||
+        (e = mnb::launch_repack(g, (const uint8_t *)q_nat, s_nat, (const uint8_t *)z_nat, w->q_t, w->s_t, w->zp_t,
+                                ctx->stream)) != hipSuccess ||
+        (e = hipStreamSynchronize(ctx->stream)) != hipSuccess) {
+        cleanup_all();
+        return hip_fail(e, "prepare");
+    }
+    cleanup_tmp();
+    w->bytes = (int64_t)(q_t_bytes + s_t_bytes + z_t_bytes);
+    ctx->live_weights++;
+    *out = w;
+    return ok();
+}
+
+int32_t mnb_weight_destroy(mnb_weight *w) {
+    if (!w) return ok();
+    DeviceGuard guard(w->ctx->device);
+    hipError_t first = hipStreamSynchronize(w->ctx->stream);
+    hipError_t e;
+    if (w->q_t && (e = hipFree(w->q_t)) != hipSuccess && first == hipSuccess) first = e;
+    if (w->s_t && (e = hipFree(w->s_t)) != hipSuccess && first == hipSuccess) first = e;
+    if (w->zp_t && (e = hipFree(w->zp_t)) != hipSuccess && first == hipSuccess) first = e;
+    w->ctx->live_weights--;
+    delete w;
+    if (first != hipSuccess) return hip_fail(first, "close");
+    return ok();
+}
+
+int32_t mnb_weight_shape(const mnb_weight *w, int32_t *N, int32_t *K, int32_t *block_size) {
+    if (!w) return fail(MNB_ERR_INVALID_STATE, "Kernel not prepared");
+    if (N) *N = w->g.N;
+    if (K) *K = w->g.K;
+    if (block_size) *block_size = w->g.bs;
+    return ok();
+}
+
+int64_t mnb_weight_device_bytes(const mnb_weight *w) { return w ? w->bytes : 0; }
+
+int32_t mnb_supports_batch(const mnb_weight *w) { return w ? 1 : 0; }
+
+int32_t mnb_max_batch_rows(void) { return std::numeric_limits<int32_t>::max() / 2; }
+
+int32_t mnb_matmul(mnb_context *ctx, const mnb_weight *w, int32_t M, const void *x, int32_t x_type, int64_t x_elems,
+                   void *y, int32_t y_type, int64_t y_elems, uint32_t flags, void *stream) {
+    if (!ctx || !w) return fail(MNB_ERR_INVALID_STATE, "Kernel not prepared");
+    if (w->ctx != ctx) return fail(MNB_ERR_INVALID_ARGUMENT, "weight belongs to another context");
+    if (flags & ~(MNB_HOST_MEMORY | MNB_ACCUMULATE)) return fail(MNB_ERR_INVALID_ARGUMENT, "unknown flags 0x%x", flags);
+    if ((x_type != MNB_F16 && x_type != MNB_F32) || (y_type != MNB_F16 && y_type != MNB_F32))
+        return fail(MNB_ERR_INVALID_ARGUMENT, "x_type/y_type must be MNB_F16 or MNB_F32");
+    const WeightGeom &g = w->g;
+    if (M < 1 || M > mnb_max_batch_rows()) return fail(MNB_ERR_INVALID_ARGUMENT, "M out of range [1, %d]: %d", mnb_max_batch_rows(), M);
+    if (!x || !y) return fail(MNB_ERR_INVALID_ARGUMENT, "x and y must not be null");
+    const int64_t MK = (int64_t)M * g.K, MN = (int64_t)M * g.N;
+    if (M == 1 && (flags & MNB_HOST_MEMORY) && x_elems != g.K)
+        return fail(MNB_ERR_INVALID_ARGUMENT, "Input length %lld != K=%d", (long long)x_elems, g.K);
+    if (x_elems < MK) return fail(MNB_ERR_INVALID_ARGUMENT, "xBatch too short: %lld < %lld", (long long)x_elems, (long long)MK);
+    if (y_elems < MN) return fail(MNB_ERR_INVALID_ARGUMENT, "outBatch too short: %lld < %lld", (long long)y_elems, (long long)MN);
+
+    const char *op = M == 1 ? "matvec" : "matmulBatch";
+    DeviceGuard guard(ctx->device);
+    hipStream_t s = (flags & MNB_HOST_MEMORY) || !stream ? ctx->stream : (hipStream_t)stream;
+    const bool host = (flags & MNB_HOST_MEMORY) != 0;
+    const int32_t ldx_pad = (g.K + 7) & ~7;
+    hipError_t e;
+
+    // activations: fp16 rows with a stride that is a multiple of 8 and 16-byte alignment
+    const _Float16 *xd = nullptr;
+    int32_t ldx = g.K;
+    const bool direct_ok = x_type == MNB_F16 && (g.K % 8) == 0;
+    if (host) {
+        if (direct_ok) {
+            if ((e = ensure(&ctx->stage_x, &ctx->stage_x_cap, (size_t)MK * 2)) != hipSuccess ||
+                (e = hipMemcpyAsync(ctx->stage_x, x, (size_t)MK * 2, hipMemcpyHostToDevice, s)) != hipSuccess)
+                return hip_fail(e, op);
+        } else {
+            if ((e = ensure(&ctx->stage_raw, &ctx->stage_raw_cap, (size_t)MK * dtype_size(x_type))) != hipSuccess ||
+                (e = ensure(&ctx->stage_x, &ctx->stage_x_cap, (size_t)M * ldx_pad * 2)) != hipSuccess ||
+                (e = hipMemcpyAsync(ctx->stage_raw, x, (size_t)MK * dtype_size(x_type), hipMemcpyHostToDevice, s)) != hipSuccess ||
+                (e = mnb::launch_stage_x(ctx->stage_raw, x_type, M, g.K, ldx_pad, (_Float16 *)ctx->stage_x, s)) != hipSuccess)
+                return hip_fail(e, op);
+            ldx = ldx_pad;
+        }
+        xd = (const _Float16 *)ctx->stage_x;
+    } else if (direct_ok && ((uintptr_t)x & 15u) == 0) {
+        xd = (const _Float16 *)x;
+    } else {
+        if ((e = ensure(&ctx->stage_x, &ctx->stage_x_cap, (size_t)M * ldx_pad * 2)) != hipSuccess ||
+            (e = mnb::launch_stage_x(x, x_type, M, g.K, ldx_pad, (_Float16 *)ctx->stage_x, s)) != hipSuccess)
+            return hip_fail(e, op);
+        xd = (const _Float16 *)ctx->stage_x;
+        ldx = ldx_pad;
+    }
+
+    void *yd = y;
+    const size_t y_bytes = (size_t)MN * dtype_size(y_type);
+    if (host) {
+        if ((e = ensure(&ctx->stage_y, &ctx->stage_y_cap, y_bytes)) != hipSuccess) return hip_fail(e, op);
+        yd = ctx->stage_y;
+        if ((flags & MNB_ACCUMULATE) &&
+            (e = hipMemcpyAsync(yd, y, y_bytes, hipMemcpyHostToDevice, s)) != hipSuccess)
+            return hip_fail(e, op);
+    }
+
+    mnb::MatmulArgs a;
+    a.x = xd;
+    a.ldx = ldx;
+    a.kx = ldx_pad;
+    a.M = M;
+    a.y = yd;
+    a.y_type = y_type;
+    a.accumulate = (flags & MNB_ACCUMULATE) ? 1 : 0;
+    e = M <= mnb::kSkinnyMaxM ? mnb::launch_gemv(w, a, ctx->cu_count, s) : mnb::launch_gemm(w, a, ctx->cu_count, s);
+    if (e != hipSuccess) return hip_fail(e, op);
+
+    if (host) {
+        if ((e = hipMemcpyAsync(y, yd, y_bytes, hipMemcpyDeviceToHost, s)) != hipSuccess ||
+            (e = hipStreamSynchronize(s)) != hipSuccess)
+            return hip_fail(e, op);
+    }
+    return ok();
+}
+
+int32_t mnb_dequantize(mnb_context *ctx, const mnb_weight *w, void *out, int32_t out_type, int64_t out_elems,
+                       uint32_t flags, void *stream) {
+    if (!ctx || !w) return fail(MNB_ERR_INVALID_STATE, "Kernel not prepared");
+    if (w->ctx != ctx) return fail(MNB_ERR_INVALID_ARGUMENT, "weight belongs to another context");
+    if (!out) return fail(MNB_ERR_INVALID_ARGUMENT, "out must not be null");
+    if (out_type != MNB_F16 && out_type != MNB_F32) return fail(MNB_ERR_INVALID_ARGUMENT, "out_type must be MNB_F16 or MNB_F32");
+    if (flags & ~MNB_HOST_MEMORY) return fail(MNB_ERR_INVALID_ARGUMENT, "unknown flags 0x%x", flags);
+    const int64_t NK = (int64_t)w->g.N * w->g.K;
+    if (out_elems < NK) return fail(MNB_ERR_INVALID_ARGUMENT, "out too short: %lld < N*K = %lld", (long long)out_elems, (long long)NK);
+    DeviceGuard guard(ctx->device);
+    const bool host = (flags & MNB_HOST_MEMORY) != 0;
+    hipStream_t s = host || !stream ? ctx->stream : (hipStream_t)stream;
+    const size_t bytes = (size_t)NK * dtype_size(out_type);
+    hipError_t e;
+    void *od = out;
+    if (host) {
+        if ((e = ensure(&ctx->stage_y, &ctx->stage_y_cap, bytes)) != hipSuccess) return hip_fail(e, "dequantizeInt4");
+        od = ctx->stage_y;
+    }
+    if ((e = mnb::launch_dequant(w, od, out_type, s)) != hipSuccess) return hip_fail(e, "dequantizeInt4");
+    if (host) {
+        if ((e = hipMemcpyAsync(out, od, bytes, hipMemcpyDeviceToHost, s)) != hipSuccess ||
+            (e = hipStreamSynchronize(s)) != hipSuccess)
+            return hip_fail(e, "dequantizeInt4");
+    }
+    return ok();
+}
+
+int32_t mnb_device_alloc(mnb_context *ctx, int64_t bytes, void **out) {
+    if (!ctx || !out) return fail(MNB_ERR_INVALID_ARGUMENT, "context and out must not be null");
+    if (bytes < 0) return fail(MNB_ERR_INVALID_ARGUMENT, "negative size");
+    DeviceGuard guard(ctx->device);
+    hipError_t e = dev_alloc(out, (size_t)bytes);
+    if (e != hipSuccess) return hip_fail(e, "alloc");
+    return ok();
+}
+
+int32_t mnb_device_free(mnb_context *ctx, void *ptr) {
+    if (!ctx) return fail(MNB_ERR_INVALID_ARGUMENT, "context must not be null");
+    if (!ptr) return ok();
+    DeviceGuard guard(ctx->device);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess) e = hipFree(ptr);
+    if (e != hipSuccess) return hip_fail(e, "free");
+    return ok();
+}
+
+int32_t mnb_memcpy(mnb_context *ctx, void *dst, const void *src, int64_t bytes, int32_t kind) {
+    if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(MNB_ERR_INVALID_ARGUMENT, "null argument");
+    if (bytes < 0) return fail(MNB_ERR_INVALID_ARGUMENT, "negative size");
+    hipMemcpyKind k;
+    switch (kind) {
+        case MNB_COPY_H2D: k = hipMemcpyHostToDevice; break;
+        case MNB_COPY_D2H: k = hipMemcpyDeviceToHost; break;
+        case MNB_COPY_D2D: k = hipMemcpyDeviceToDevice; break;
+        default: return fail(MNB_ERR_INVALID_ARGUMENT, "unknown copy kind %d", kind);
+    }
+    DeviceGuard guard(ctx->device);
+    hipError_t e = hipMemcpyAsync(dst, src, (size_t)bytes, k, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "copy");
+    return ok();
+}
+
+int32_t mnb_synchronize(mnb_context *ctx) {
+    if (!ctx) return fail(MNB_ERR_INVALID_ARGUMENT, "context must not be null");
+    DeviceGuard guard(ctx->device);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "synchronize");
+    return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,80 @@
+// mnb_device.h -- device-side helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mnb_internal.h"
+
+namespace mnb {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ half2_t as_half2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// fp16 pair constants used by the nibble -> fp16 conversion.
+//   (0x6400 | q) is the fp16 value 1024 + q   (q in bits 0..3)
+//   (0x6400 | q<<4) is 1024 + 16 q; times 1/16 it is 64 + q exactly.
+__device__ __forceinline__ uint32_t bias_lo_pair(uint32_t zp) {   // fp16 (1024 + zp) in both halves
+    return 0x64006400u | (zp * 0x00010001u);
+}
+__device__ __forceinline__ uint32_t bias_hi_pair(uint32_t zp) {   // fp16 (64 + zp) in both halves
+    return 0x54005400u | ((zp << 4) * 0x00010001u);
+}
+
+// Eight packed nibbles of one dword of the tiled layout -> eight fp16 values
+// (q_i - zp), exact.  Result halves are k0..k7 in MFMA operand order.
+//   d & 0x000F000F             -> (k0, k1) as 1024+q   -> minus (1024+zp)
+//   d & 0x00F000F0             -> (k2, k3) as 1024+16q -> /16 minus (64+zp)
+//   (d>>8) & 0x000F000F        -> (k4, k5)
+//   (d>>8) & 0x00F000F0        -> (k6, k7)
+// Every intermediate is an fp16 integer (or integer + 1024) below 2048, so
+// the subtraction and the fused 1/16 scaling are exact.
+__device__ __forceinline__ half8_t unpack_q_minus_zp(uint32_t d, uint32_t blo, uint32_t bhi) {
+    const half2_t lo = as_half2(blo);
+    const half2_t hi = as_half2(bhi);
+    const half2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const uint32_t d8 = d >> 8;
+    half2_t p0 = as_half2((d & 0x000F000Fu) | 0x64006400u) - lo;
+    half2_t p1 = as_half2((d & 0x00F000F0u) | 0x64006400u) * sixteenth - hi;
+    half2_t p2 = as_half2((d8 & 0x000F000Fu) | 0x64006400u) - lo;
+    half2_t p3 = as_half2((d8 & 0x00F000F0u) | 0x64006400u) * sixteenth - hi;
+    half8_t r;
+    r[0] = p0[0]; r[1] = p0[1];
+    r[2] = p1[0]; r[3] = p1[1];
+    r[4] = p2[0]; r[5] = p2[1];
+    r[6] = p3[0]; r[7] = p3[1];
+    return r;
+}
+
+// The i-th nibble (low first) of a zero-point entry.
+__device__ __forceinline__ uint32_t zp_nibble(uint32_t zbits, int i) { return (zbits >> (4 * i)) & 0xFu; }
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T v) { return (float)v; }
+
+__device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Load SPS consecutive scales (SPS in {1,2,4,8}) as floats.
+template <typename ScaleT, int SPS>
+__device__ __forceinline__ void load_scales(const ScaleT *p, float (&s)[SPS]) {
+#pragma unroll
+    for (int i = 0; i < SPS; ++i) s[i] = (float)p[i];
+}
+
+// Load one zero-point entry of ZB bytes.
+template <int ZB>
+__device__ __forceinline__ uint32_t load_zp(const uint8_t *p) {
+    if constexpr (ZB == 1) return *p;
+    else if constexpr (ZB == 2) return *(const uint16_t *)p;
+    else return *(const uint32_t *)p;
+}
+
+}  // namespace mnb

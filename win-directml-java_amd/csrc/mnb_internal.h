@@ -1,0 +1,112 @@
+// mnb_internal.h -- shared definitions of libmnb_hip: the HBM layout of a
+// resident weight, the context, and the kernel launchers.
+//
+// HBM layout of one weight (N rows, kb blocks of bs nibbles per row):
+//
+//   The weight is cut into tiles of 16 rows x 128 k ("n-tile" x "super-tile"),
+//   NT = ceil(N/16) n-tiles and ST = ceil(kb*bs/128) super-tiles per row.
+//   Each tile is 1 KiB of packed nibbles stored so that ONE 16-byte load per
+//   lane of a 64-lane wavefront brings a whole tile into registers already in
+//   the operand order of v_mfma_f32_16x16x32_f16:
+//
+//     byte offset of tile (nt, st)   = ((nt*ST + st) * 64) * 16
+//     lane l = g*16 + r  (r = row within the tile, g = 8-k group)  -> 16 bytes
+//     dword j (0..3) of that lane    = 8 nibbles of row nt*16+r,
+//                                      k = st*128 + 32*j + 8*g + (0..7)
+//     nibble order inside the dword  = k0,k2,k4,k6 in bits 0..15 and
+//                                      k1,k3,k5,k7 in bits 16..31, so that
+//                                      (d & 0x000F000F) holds (k0,k1) in the two
+//                                      fp16 halves, (d & 0x00F000F0) holds (k2,k3),
+//                                      and the same on d >> 8 gives (k4,k5),(k6,k7).
+//
+//   Scales: [NT][ST][16][SPS] of fp16 (or fp32 when the caller's fp32 scales
+//   are not all fp16-exact), SPS = max(1, 128/bs) scales per row per
+//   super-tile; entry i is the scale of block (st*128)/bs + i.
+//   Zero points (optional): [NT][ST][16] entries of ZB = max(1, SPS/2) bytes,
+//   nibble i (low nibble first) belongs to the same block as scale i.
+//   Rows >= N, blocks >= kb and k >= kb*bs are stored as zero nibbles, zero
+//   scales and zero zero-points, so they contribute exact zeros.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mnb.h"
+
+namespace mnb {
+
+constexpr int kTileRows = 16;     // rows per n-tile (MFMA N dimension)
+constexpr int kTileK = 128;       // k per super-tile (4 MFMA K-steps of 32)
+constexpr int kTileBytes = 1024;  // packed bytes per tile
+
+struct WeightGeom {
+    int32_t N = 0, K = 0, bs = 0;
+    int32_t kb = 0, Kpad = 0;     // blocks per row, kb*bs
+    int32_t NT = 0, ST = 0;       // n-tiles, super-tiles
+    int32_t SPS = 0, ZB = 0;      // scales per row per super-tile, zp bytes per row per super-tile
+    int32_t scale_f32 = 0;        // 1: device scales are fp32
+    int32_t has_zp = 0;           // 0: implicit zero point 8
+};
+
+WeightGeom make_geom(int32_t N, int32_t K, int32_t bs);
+
+}  // namespace mnb
+
+struct mnb_context {
+    int32_t device = 0;
+    hipStream_t stream = nullptr;
+    int32_t cu_count = 0;
+    int64_t live_weights = 0;
+    // staging buffers for host-memory calls and for x conversion (grown on demand)
+    void *stage_raw = nullptr;
+    size_t stage_raw_cap = 0;
+    void *stage_x = nullptr;
+    size_t stage_x_cap = 0;
+    void *stage_y = nullptr;
+    size_t stage_y_cap = 0;
+    mnb_device_info info{};
+};
+
+struct mnb_weight {
+    mnb_context *ctx = nullptr;
+    mnb::WeightGeom g;
+    void *q_t = nullptr;    // tiled packed nibbles
+    void *s_t = nullptr;    // tiled scales
+    void *zp_t = nullptr;   // tiled zero points (nullptr when implicit 8)
+    int64_t bytes = 0;
+};
+
+namespace mnb {
+
+// Kernel launchers (defined in the .hip files).  All take device pointers and
+// enqueue on `stream`; they return the launch status.
+
+// natural layout (device copies of the caller's tensors) -> tiled layout
+hipError_t launch_repack(const WeightGeom &g, const uint8_t *q_nat, const void *s_nat, const uint8_t *zp_flat,
+                         void *q_t, void *s_t, void *zp_t, hipStream_t stream);
+
+// x[M, K] (f16 or f32, row stride K) -> fp16 [M, ldx] with zeros in k in [K, ldx)
+hipError_t launch_stage_x(const void *x, int32_t x_type, int32_t M, int32_t K, int32_t ldx, _Float16 *out,
+                          hipStream_t stream);
+
+// out[N, K] = dequantized weight (f32 or f16)
+hipError_t launch_dequant(const mnb_weight *w, void *out, int32_t out_type, hipStream_t stream);
+
+// y[M, N] (=|+=) x[M, kx] W^T; x fp16 with row stride ldx (multiple of 8,
+// 16-byte aligned), k >= kx contributes zero (kx = K rounded up to 8, the
+// x values in [K, kx) must be zero).
+struct MatmulArgs {
+    const _Float16 *x;
+    int32_t ldx, kx, M;
+    void *y;
+    int32_t y_type;
+    int32_t accumulate;
+};
+hipError_t launch_gemv(const mnb_weight *w, const MatmulArgs &a, int32_t cu_count, hipStream_t stream);
+hipError_t launch_gemm(const mnb_weight *w, const MatmulArgs &a, int32_t cu_count, hipStream_t stream);
+
+// largest M handled by the skinny (GEMV-style) kernel
+constexpr int kSkinnyMaxM = 16;
+
+}  // namespace mnb
