@@ -105,7 +105,8 @@ def per_launch_times(torch, launcher, stream, reps=3):
     for r in range(reps):
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
         with torch.cuda.stream(stream):
-            torch.cuda._sleep(int(40e6))
+            if hasattr(torch.cuda, "_sleep"):
+                torch.cuda._sleep(int(40e6))
             for i in range(n):
                 evs[i][0].record(stream)
                 launcher.run([i])

@@ -183,7 +183,11 @@ __global__ void dequant_kernel(WeightGeom g, const uint32_t *__restrict__ q_t, c
     for (int i = 0; i < 8; ++i) {
         if (k0 + i < g.K) {
             const int w = (int)tiled_nibble(t, i) - z;
-            const float v = (float)w * scale;
+            float v = (float)w * scale;
+            // Keep the binary32 product in a register before the fp16 rounding:
+            // otherwise the multiply and the conversion are fused into
+            // v_fma_mix(scale, w, +0), which turns a -0 product into +0.
+            asm volatile("" : "+v"(v));
             o[i] = (OutT)v;
         }
     }

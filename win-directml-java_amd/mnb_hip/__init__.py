@@ -92,6 +92,14 @@ def load() -> ctypes.CDLL:
         return _lib
     if not os.path.exists(LIB_PATH):
         raise MnbError(MNB_ERR_NO_DEVICE, "libmnb_hip.so is not built (run __graft_entry__.build())")
+    # One HIP runtime per process: PyTorch-ROCm ships its own libamdhip64 (soname
+    # libamdhip64.so.7) and loads it under another file name.  Loaded first, it
+    # also satisfies this library's libamdhip64.so.7 dependency; loaded after
+    # this library it would start a second runtime that sees no device.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = ctypes.CDLL(LIB_PATH)
     vp, i32, i64, u32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32
     sig = {
