@@ -35,21 +35,32 @@ __device__ __forceinline__ uint32_t bias_hi_pair(uint32_t zp) {   // fp16 (64 + 
 //   (d>>8) & 0x00F000F0        -> (k6, k7)
 // Every intermediate is an fp16 integer (or integer + 1024) below 2048, so
 // the subtraction and the fused 1/16 scaling are exact.
-__device__ __forceinline__ half8_t unpack_q_minus_zp(uint32_t d, uint32_t blo, uint32_t bhi) {
+//
+// `k6400` must hold 0x64006400 in a VGPR (see vgpr_const): gfx9 VOP3
+// instructions take no literal operand and at most one SGPR, so with the
+// mask in an SGPR and this constant in a VGPR each (d & mask) | 0x64006400
+// is a single v_and_or_b32.
+__device__ __forceinline__ half8_t unpack_q_minus_zp(uint32_t d, uint32_t blo, uint32_t bhi, uint32_t k6400) {
     const half2_t lo = as_half2(blo);
     const half2_t hi = as_half2(bhi);
     const half2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
     const uint32_t d8 = d >> 8;
-    half2_t p0 = as_half2((d & 0x000F000Fu) | 0x64006400u) - lo;
-    half2_t p1 = as_half2((d & 0x00F000F0u) | 0x64006400u) * sixteenth - hi;
-    half2_t p2 = as_half2((d8 & 0x000F000Fu) | 0x64006400u) - lo;
-    half2_t p3 = as_half2((d8 & 0x00F000F0u) | 0x64006400u) * sixteenth - hi;
+    half2_t p0 = as_half2((d & 0x000F000Fu) | k6400) - lo;
+    half2_t p1 = as_half2((d & 0x00F000F0u) | k6400) * sixteenth - hi;
+    half2_t p2 = as_half2((d8 & 0x000F000Fu) | k6400) - lo;
+    half2_t p3 = as_half2((d8 & 0x00F000F0u) | k6400) * sixteenth - hi;
     half8_t r;
     r[0] = p0[0]; r[1] = p0[1];
     r[2] = p1[0]; r[3] = p1[1];
     r[4] = p2[0]; r[5] = p2[1];
     r[6] = p3[0]; r[7] = p3[1];
     return r;
+}
+
+// A constant the compiler must keep in a VGPR (opaque to constant folding).
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
+    asm volatile("" : "+v"(c));
+    return c;
 }
 
 // The i-th nibble (low first) of a zero-point entry.

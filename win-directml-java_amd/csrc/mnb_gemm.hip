@@ -49,6 +49,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
     const int m0 = blockIdx.x * BM;
     const int nt0 = blockIdx.y * BNT;
     const ScaleT *sbase = (const ScaleT *)p.s_t;
+    const uint32_t k6400 = vgpr_const(0x64006400u);
 
     u32x4_t a_reg[A_PER_T];
     u32x4_t b_reg[B_PER_T];
@@ -105,8 +106,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int si = SPS == 8 ? 2 * j + (g2 >> 1) : (SPS == 1 ? 0 : j / (4 / SPS));
-                const uint32_t z = zp_nibble(b_z[i], si);
-                half8_t w = unpack_q_minus_zp(b_reg[i][j], bias_lo_pair(z), bias_hi_pair(z));
+                const uint32_t z = HAS_ZP ? zp_nibble(b_z[i], si) : 8u;
+                half8_t w = unpack_q_minus_zp(b_reg[i][j], bias_lo_pair(z), bias_hi_pair(z), k6400);
                 if constexpr (sizeof(ScaleT) == 2) {
                     w = w * (_Float16)b_s[i][si];
                 } else {

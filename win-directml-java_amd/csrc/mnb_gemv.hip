@@ -42,17 +42,49 @@ __device__ __forceinline__ void store_y(void *y, size_t idx, float v, bool accum
     }
 }
 
-template <typename ScaleT, bool HAS_ZP, bool M1, int SPS>
+// Load the SPS scales of one row of one tile (SPS * sizeof(ScaleT) bytes,
+// naturally aligned in the tiled layout) with the widest vector load.
+template <typename ScaleT, int SPS>
+__device__ __forceinline__ void load_scale_row(const ScaleT *p, ScaleT (&s)[SPS]) {
+    constexpr int BYTES = SPS * (int)sizeof(ScaleT);
+    if constexpr (BYTES == 2) {
+        uint16_t v = *(const uint16_t *)p;
+        __builtin_memcpy(&s, &v, 2);
+    } else if constexpr (BYTES == 4) {
+        uint32_t v = *(const uint32_t *)p;
+        __builtin_memcpy(&s, &v, 4);
+    } else if constexpr (BYTES == 8) {
+        u32x2_t v = *(const u32x2_t *)p;
+        __builtin_memcpy(&s, &v, 8);
+    } else if constexpr (BYTES == 16) {
+        u32x4_t v = *(const u32x4_t *)p;
+        __builtin_memcpy(&s, &v, 16);
+    } else {
+        u32x4_t v0 = ((const u32x4_t *)p)[0], v1 = ((const u32x4_t *)p)[1];
+        __builtin_memcpy(&s, &v0, 16);
+        __builtin_memcpy((char *)&s + 16, &v1, 16);
+    }
+}
+
+// M1: x has one row, staged once per workgroup in LDS (A operand = x
+// broadcast to all 16 MFMA rows).  !M1: up to 16 rows read from global
+// memory (rows >= M repeat row M-1 and their results are discarded).
+// STW: super-tiles per wave; all of a wave's weight, scale and zero-point
+// loads are issued before any arithmetic.
+template <typename ScaleT, bool HAS_ZP, bool M1, int SPS, int STW>
 __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
     constexpr int ZB = SPS <= 2 ? 1 : SPS / 2;
-    __shared__ float4_t red[16 * 64];
+    extern __shared__ __align__(16) unsigned char smem[];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int W = blockDim.x >> 6;
+    float4_t *red = (float4_t *)smem;                              // [W][64]
+    // M1: each wave's slice of x (STW*128 halves) in a wave-private region
+    _Float16 *xs = (_Float16 *)(smem + (size_t)W * 64 * sizeof(float4_t)) + wave * (STW * kTileK);
     const int r = lane & 15, gg = lane >> 4;
     const int nt = blockIdx.x;
-    const int st0 = (wave * p.ST) / W, st1 = ((wave + 1) * p.ST) / W;
+    const int nchunks = (p.ST + STW - 1) / STW;
 
     const size_t tile0 = (size_t)nt * p.ST;
     const u32x4_t *qp = p.q_t + tile0 * 64 + lane;
@@ -61,53 +93,103 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
     const int m = M1 ? 0 : (r < p.M ? r : p.M - 1);
     const _Float16 *xr = p.x + (size_t)m * p.ldx + 8 * gg;
     const half8_t zero8 = {};
+    const u32x4_t zero4 = {0u, 0u, 0u, 0u};
+    const uint32_t k6400 = vgpr_const(0x64006400u);
+
+    u32x4_t raw[STW];
+    ScaleT sv[STW][SPS];
+    uint32_t zb[STW];
+    // Straight-line loads (no per-lane branches, so the compiler's wait
+    // counters stay exact).  A super-tile index past the end is clamped to the
+    // last tile: its k range lies at or beyond kx, where x is zero, so the
+    // repeated tile contributes exactly zero.
+    auto issue = [&](int c) {
+#pragma unroll
+        for (int t = 0; t < STW; ++t) {
+            const int st = min(c * STW + t, p.ST - 1);
+            raw[t] = qp[(size_t)st * 64];
+            load_scale_row<ScaleT, SPS>(sp + (size_t)st * kTileRows * SPS, sv[t]);
+            if constexpr (HAS_ZP) zb[t] = load_zp<ZB>(zpp + (size_t)st * kTileRows * ZB);
+            else zb[t] = 0x88888888u;
+        }
+    };
+
+    // M1: one coalesced 16-byte load per lane brings the wave's x slice
+    // (issued before the weights, so it is the first to arrive).
+    auto load_x_slice = [&](int c) -> u32x4_t {
+        const int k = c * STW * kTileK + 8 * lane;
+        const u32x4_t v = *(const u32x4_t *)(p.x + min(k, p.kx - 8));
+        return (lane < STW * (kTileK / 8) && k < p.kx) ? v : zero4;
+    };
+
+    u32x4_t xv = zero4;
+    if constexpr (M1) xv = load_x_slice(wave);
+    issue(wave);   // the host launches at most nchunks waves, so wave < nchunks
+    __builtin_amdgcn_sched_barrier(0);   // every load of the chunk is issued before any arithmetic
 
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    auto compute_chunk = [&](int c) {
+        if constexpr (M1) {
+            // wave-private LDS: a wave's LDS accesses complete in order, no barrier needed
+            if (lane < STW * (kTileK / 8)) ((u32x4_t *)xs)[lane] = xv;
+        }
+#pragma unroll
+        for (int t = 0; t < STW; ++t) {
+            half8_t xa[4];
+            const int kst = (c * STW + t) * kTileK;
+            if constexpr (M1) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xa[j] = *(const half8_t *)(xs + t * kTileK + 32 * j + 8 * gg);
+            } else if (kst + kTileK <= p.kx) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xa[j] = *(const half8_t *)(xr + kst + 32 * j);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    xa[j] = kst + 32 * j + 8 * gg < p.kx ? *(const half8_t *)(xr + kst + 32 * j) : zero8;
+            }
+            if constexpr (SPS == 8) {
+                // bs = 16: the lane's 8 k lie in block 2j + gg/2; fold the scale.
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int i = 2 * j + (gg >> 1);
+                    const uint32_t z = HAS_ZP ? zp_nibble(zb[t], i) : 8u;
+                    half8_t b = unpack_q_minus_zp(raw[t][j], bias_lo_pair(z), bias_hi_pair(z), k6400);
+                    b = b * (_Float16)(float)sv[t][i];
+                    acc = mfma16x16x32(xa[j], b, acc);
+                }
+            } else {
+                constexpr int KPB = 4 / SPS;   // 32-k steps per scale block inside the super-tile
+#pragma unroll
+                for (int i = 0; i < SPS; ++i) {
+                    const uint32_t z = HAS_ZP ? zp_nibble(zb[t], i) : 8u;
+                    const uint32_t blo = bias_lo_pair(z), bhi = bias_hi_pair(z);
+                    float4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int u = 0; u < KPB; ++u) {
+                        const int j = i * KPB + u;
+                        d = mfma16x16x32(xa[j], unpack_q_minus_zp(raw[t][j], blo, bhi, k6400), d);
+                    }
+                    const float s = (float)sv[t][i];
+                    acc[0] = fmaf(s, d[0], acc[0]);
+                    if constexpr (!M1) {
+                        acc[1] = fmaf(s, d[1], acc[1]);
+                        acc[2] = fmaf(s, d[2], acc[2]);
+                        acc[3] = fmaf(s, d[3], acc[3]);
+                    }
+                }
+            }
+        }
+    };
 
-    for (int st = st0; st < st1; ++st) {
-        const u32x4_t raw = qp[(size_t)st * 64];
-        float s[SPS];
-        load_scales<ScaleT, SPS>(sp + (size_t)st * kTileRows * SPS, s);
-        uint32_t zb = 0x88888888u;
-        if constexpr (HAS_ZP) zb = load_zp<ZB>(zpp + (size_t)st * kTileRows * ZB);
-        half8_t xa[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int k = st * kTileK + 32 * j;
-            xa[j] = (k + 8 * gg < p.kx) ? *(const half8_t *)(xr + k) : zero8;
-        }
-        if constexpr (SPS == 8) {
-            // bs = 16: the lane's 8 k lie in block 2j + gg/2; fold the scale.
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int i = 2 * j + (gg >> 1);
-                const uint32_t z = zp_nibble(zb, i);
-                half8_t b = unpack_q_minus_zp(raw[j], bias_lo_pair(z), bias_hi_pair(z));
-                b = b * (_Float16)s[i];
-                acc = mfma16x16x32(xa[j], b, acc);
-            }
-        } else {
-            constexpr int KPB = 4 / SPS;   // 32-k steps per scale block inside the super-tile
-#pragma unroll
-            for (int i = 0; i < SPS; ++i) {
-                const uint32_t z = zp_nibble(zb, i);
-                const uint32_t blo = bias_lo_pair(z), bhi = bias_hi_pair(z);
-                float4_t d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int t = 0; t < KPB; ++t) {
-                    const int j = i * KPB + t;
-                    d = mfma16x16x32(xa[j], unpack_q_minus_zp(raw[j], blo, bhi), d);
-                }
-                if constexpr (M1) {
-                    acc[0] = fmaf(s[i], d[0], acc[0]);
-                } else {
-                    acc[0] = fmaf(s[i], d[0], acc[0]);
-                    acc[1] = fmaf(s[i], d[1], acc[1]);
-                    acc[2] = fmaf(s[i], d[2], acc[2]);
-                    acc[3] = fmaf(s[i], d[3], acc[3]);
-                }
-            }
-        }
+    // The first chunk is straight-line code after its loads; further chunks
+    // (K > 16 waves x STW x 128) loop.
+    compute_chunk(wave);
+    for (int c = wave + W; c < nchunks; c += W) {
+        if constexpr (M1) xv = load_x_slice(c);
+        issue(c);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_chunk(c);
     }
 
     if (W > 1) {
@@ -145,33 +227,49 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
     }
 }
 
-template <typename ScaleT, bool HAS_ZP, bool M1>
-static hipError_t gemv_sps(const WeightGeom &g, dim3 grid, dim3 block, const GemvParams &p, hipStream_t s) {
-    switch (g.SPS) {
-        case 1: hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, M1, 1>), grid, block, 0, s, p); break;
-        case 2: hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, M1, 2>), grid, block, 0, s, p); break;
-        case 4: hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, M1, 4>), grid, block, 0, s, p); break;
-        case 8: hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, M1, 8>), grid, block, 0, s, p); break;
+struct GemvLaunch {
+    dim3 grid, block;
+    size_t lds;
+    int stw;
+};
+
+template <typename ScaleT, bool HAS_ZP, bool M1, int SPS>
+static hipError_t gemv_stw(const GemvLaunch &L, const GemvParams &p, hipStream_t s) {
+    switch (L.stw) {
+        case 2: hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, M1, SPS, 2>), L.grid, L.block, L.lds, s, p); break;
+        case 4: hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, M1, SPS, 4>), L.grid, L.block, L.lds, s, p); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
+template <typename ScaleT, bool HAS_ZP, bool M1>
+static hipError_t gemv_sps(const WeightGeom &g, const GemvLaunch &L, const GemvParams &p, hipStream_t s) {
+    switch (g.SPS) {
+        case 1: return gemv_stw<ScaleT, HAS_ZP, M1, 1>(L, p, s);
+        case 2: return gemv_stw<ScaleT, HAS_ZP, M1, 2>(L, p, s);
+        case 4: return gemv_stw<ScaleT, HAS_ZP, M1, 4>(L, p, s);
+        case 8: return gemv_stw<ScaleT, HAS_ZP, M1, 8>(L, p, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 template <typename ScaleT>
-static hipError_t gemv_zp(const WeightGeom &g, dim3 grid, dim3 block, const GemvParams &p, bool m1, hipStream_t s) {
-    if (g.has_zp) return m1 ? gemv_sps<ScaleT, true, true>(g, grid, block, p, s) : gemv_sps<ScaleT, true, false>(g, grid, block, p, s);
-    return m1 ? gemv_sps<ScaleT, false, true>(g, grid, block, p, s) : gemv_sps<ScaleT, false, false>(g, grid, block, p, s);
+static hipError_t gemv_zp(const WeightGeom &g, const GemvLaunch &L, const GemvParams &p, bool m1, hipStream_t s) {
+    if (g.has_zp) return m1 ? gemv_sps<ScaleT, true, true>(g, L, p, s) : gemv_sps<ScaleT, true, false>(g, L, p, s);
+    return m1 ? gemv_sps<ScaleT, false, true>(g, L, p, s) : gemv_sps<ScaleT, false, false>(g, L, p, s);
 }
 
-// Waves per workgroup: about three super-tiles (3 x 16 B in flight) per wave.
-static int gemv_waves(int ST) {
-    int w = (ST + 2) / 3;
-    if (w < 1) w = 1;
-    if (w > 16) w = 16;
-    return w;
+// Super-tiles per wave: 4 (4 KiB of weights in flight per wave), or 2 when
+// the grid would otherwise have fewer than 8 waves per CU.  K above
+// 16 waves x 4 x 128 = 8192 loops over further chunks per wave.
+static int gemv_stw_for(const WeightGeom &g, int cu_count) {
+    if ((g.ST + 3) / 4 <= 16 && (int64_t)g.NT * ((g.ST + 3) / 4) >= 8LL * cu_count) return 4;
+    if ((g.ST + 1) / 2 <= 16) return 2;
+    return 4;
 }
 
-hipError_t launch_gemv(const mnb_weight *w, const MatmulArgs &a, int32_t /*cu_count*/, hipStream_t stream) {
+hipError_t launch_gemv(const mnb_weight *w, const MatmulArgs &a, int32_t cu_count, hipStream_t stream) {
     const WeightGeom &g = w->g;
     if (a.M < 1 || a.M > kSkinnyMaxM) return hipErrorInvalidValue;
     GemvParams p;
@@ -187,10 +285,15 @@ hipError_t launch_gemv(const mnb_weight *w, const MatmulArgs &a, int32_t /*cu_co
     p.y = a.y;
     p.y_f16 = a.y_type == MNB_F16;
     p.accumulate = a.accumulate;
-    dim3 grid(g.NT), block(64 * gemv_waves(g.ST));
+    GemvLaunch L;
+    L.stw = gemv_stw_for(g, cu_count > 0 ? cu_count : 256);
+    int waves = (g.ST + L.stw - 1) / L.stw;
+    if (waves > 16) waves = 16;
     const bool m1 = a.M == 1;
-    return g.scale_f32 ? gemv_zp<float>(g, grid, block, p, m1, stream)
-                       : gemv_zp<_Float16>(g, grid, block, p, m1, stream);
+    L.grid = dim3(g.NT);
+    L.block = dim3(64 * waves);
+    L.lds = (size_t)waves * 64 * sizeof(float4_t) + (m1 ? (size_t)waves * L.stw * kTileK * 2 : 0);
+    return g.scale_f32 ? gemv_zp<float>(g, L, p, m1, stream) : gemv_zp<_Float16>(g, L, p, m1, stream);
 }
 
 }  // namespace mnb
