@@ -207,6 +207,19 @@ def main():
     wall, gpu = time_graph(torch, g_dec, stream, args.steps, args.warmup)
     value = bytes_step / wall / 1e9
     log("decode step: %.1f us wall, %.1f us gpu, %.1f GB/s" % (wall * 1e6, gpu * 1e6, value))
+    # the same 129 projections recorded as one group launch (independent items)
+    grp = mnb_hip.Group(ctx, list(zip(weights, xs, ys)))
+    g_grp = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        grp.run(stream.cuda_stream)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g_grp, stream=stream):
+        grp.run(stream.cuda_stream)
+    wall_g, gpu_g = time_graph(torch, g_grp, stream, args.steps, args.warmup)
+    value_group = bytes_step / wall_g / 1e9
+    log("decode step as one group launch: %.1f us wall, %.1f GB/s" % (wall_g * 1e6, value_group))
+    del g_grp
+    grp.close()
     d1 = per_launch_times(torch, dec, stream)
     achieved_gbs = bytes_step / d1.sum() / 1e9
     per_shape = {}
@@ -294,6 +307,9 @@ def main():
                                       "frac": round(kernel_tflops512 / FP16_PEAK_TFLOPS, 4),
                                       "kernel": "mnb::gemm_kernel (M=512)"},
                          "sweep_tflops": sweep},
+        "decode_step_group": {"gbs": round(value_group, 2), "ms_per_step": round(wall_g * 1e3, 4),
+                              "frac_hbm_peak": round(value_group / HBM_PEAK_GBS, 4),
+                              "note": "same 129 projections as one recorded group launch (independent items)"},
         "device_copy_gbs": round(copy_gbs, 1),
         "cpu_baseline": cpu,
     }

@@ -165,6 +165,33 @@ int32_t mnb_supports_batch(const mnb_weight *w);
  * (MNK:2361, which is 256 there). */
 int32_t mnb_max_batch_rows(void);
 
+/* A recorded group of independent products executed as ONE launch.
+ * Replaces recording several MatMulNBits dispatches into one command list
+ * without barriers between them (recordInto / recordBatchDispatchOnly,
+ * MNK:1935-2117; WarpExecutionContext.java:131-160; the batched layer
+ * submissions of Phi3GpuPipeline.java:191-231): the items may run
+ * concurrently, so no item may read another item's output.
+ * Each item: device pointers, fp16 x [M, K] (K a multiple of 8, 16-byte
+ * aligned), y [M, N] fp16 or fp32, 1 <= M <= 16; all items share the weight
+ * variant (scale type, zero points or not, block size class) and either all
+ * have M == 1 or all have M > 1.  The group keeps its own device descriptor
+ * table, so mnb_group_run allocates nothing and can be captured in a HIP graph. */
+typedef struct mnb_group mnb_group;
+typedef struct mnb_group_item {
+    const mnb_weight *weight;
+    int32_t M;
+    const void *x;
+    int32_t x_type;
+    int64_t x_elems;
+    void *y;
+    int32_t y_type;
+    int64_t y_elems;
+    uint32_t flags; /* 0 or MNB_ACCUMULATE */
+} mnb_group_item;
+int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *items, mnb_group **out);
+int32_t mnb_group_run(mnb_context *ctx, const mnb_group *group, void *stream);
+int32_t mnb_group_destroy(mnb_group *group);
+
 /* Device buffers for resident activations (WarpGpuBuffer in the reference,
  * used by MNK:1687-1832). */
 int32_t mnb_device_alloc(mnb_context *ctx, int64_t bytes, void **out);

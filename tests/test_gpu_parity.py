@@ -372,3 +372,40 @@ def test_error_paths(ctx):
         del os.environ["MNB_FAULT_INJECT"]
     w = mnb_hip.Weight(ctx, 64, 256, 32, t.q, t.scales_f16)     # recovers after the injected failure
     w.close()
+
+
+def test_group_matches_oracle_and_single_launches(ctx):
+    """Independent products recorded as one group launch."""
+    import torch
+    shapes = [(3072, 9216), (3072, 3072), (8192, 3072), (896, 1152), (3072, 3072)]
+    entries, host = [], []
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        for i, (K, N) in enumerate(shapes):
+            t = synth.make_weight(900 + i, N, K, 32)
+            w = upload(ctx, t)
+            x16 = synth.make_x(950 + i, 1, K)
+            xd = torch.from_numpy(x16).cuda()
+            yd = torch.empty((1, N), dtype=torch.float16, device="cuda")
+            entries.append((w, xd, yd))
+            host.append((t, x16))
+    torch.cuda.synchronize()
+    g = mnb_hip.Group(ctx, entries)
+    for rep in range(3):     # replays overwrite the same outputs
+        g.run(st.cuda_stream)
+        torch.cuda.synchronize()
+        for (w, xd, yd), (t, x16) in zip(entries, host):
+            rows = np.sort(np.random.default_rng(t.N).choice(t.N, min(t.N, 512), replace=False))
+            y_ref, _ = oracle_matmul(t, x16, rows)
+            y = yd.cpu().numpy()
+            assert_parity(y[:, rows], y_ref, x16, t, None, True, "group K=%d N=%d rep=%d" % (t.K, t.N, rep))
+            single = w.matmul(x16, out_dtype=np.float16)
+            assert np.max(np.abs(single.astype(np.float32) - y.astype(np.float32))) <= 2 * fp16_ulp(
+                np.abs(single.astype(np.float32)).max())
+    g.close()
+    with pytest.raises(mnb_hip.MnbError):       # mixed M classes are refused
+        mnb_hip.Group(ctx, [entries[0], (entries[1][0], torch.zeros((2, 3072), dtype=torch.float16,
+                                                                    device="cuda"),
+                                         torch.zeros((2, 3072), dtype=torch.float16, device="cuda"))])
+    for w, _, _ in entries:
+        w.close()

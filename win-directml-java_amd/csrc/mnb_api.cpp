@@ -13,7 +13,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
 #include <limits>
+#include <queue>
 #include <string>
 #include <vector>
 
@@ -469,6 +471,173 @@ int32_t mnb_dequantize(mnb_context *ctx, const mnb_weight *w, void *out, int32_t
             (e = hipStreamSynchronize(s)) != hipSuccess)
             return hip_fail(e, "dequantizeInt4");
     }
+    return ok();
+}
+
+}  // extern "C"
+
+struct mnb_group {
+    mnb_context *ctx = nullptr;
+    mnb::GemvGroupPlan plan;
+};
+
+extern "C" {
+
+int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *items, mnb_group **out) {
+    if (!out) return fail(MNB_ERR_INVALID_ARGUMENT, "out must not be null");
+    *out = nullptr;
+    if (!ctx) return fail(MNB_ERR_INVALID_STATE, "Kernel not prepared: no context");
+    if (count < 1 || count > 65535 || !items) return fail(MNB_ERR_INVALID_ARGUMENT, "count=%d must be in [1, 65535]", count);
+    std::vector<mnb::GroupItem> host((size_t)count);
+    mnb::GemvGroupPlan plan;
+    int64_t wgs = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        const mnb_group_item &it = items[i];
+        const mnb_weight *w = it.weight;
+        if (!w) return fail(MNB_ERR_INVALID_STATE, "item %d: Kernel not prepared", i);
+        if (w->ctx != ctx) return fail(MNB_ERR_INVALID_ARGUMENT, "item %d: weight belongs to another context", i);
+        const WeightGeom &g = w->g;
+        if (it.M < 1 || it.M > mnb::kSkinnyMaxM)
+            return fail(MNB_ERR_UNSUPPORTED, "item %d: M=%d; group items take 1 <= M <= %d", i, it.M, mnb::kSkinnyMaxM);
+        if (it.x_type != MNB_F16 || (g.K % 8) != 0 || ((uintptr_t)it.x & 15u) || !it.x)
+            return fail(MNB_ERR_UNSUPPORTED, "item %d: x must be 16-byte aligned fp16 with K a multiple of 8", i);
+        if ((it.y_type != MNB_F16 && it.y_type != MNB_F32) || !it.y)
+            return fail(MNB_ERR_INVALID_ARGUMENT, "item %d: y must be fp16 or fp32", i);
+        if (it.flags & ~MNB_ACCUMULATE) return fail(MNB_ERR_INVALID_ARGUMENT, "item %d: unknown flags 0x%x", i, it.flags);
+        if (it.x_elems < (int64_t)it.M * g.K || it.y_elems < (int64_t)it.M * g.N)
+            return fail(MNB_ERR_INVALID_ARGUMENT, "item %d: x or y too short", i);
+        const int m1 = it.M == 1;
+        if (i == 0) {
+            plan.scale_f32 = g.scale_f32;
+            plan.has_zp = g.has_zp;
+            plan.sps = g.SPS;
+            plan.m1 = m1;
+        } else if (plan.scale_f32 != g.scale_f32 || plan.has_zp != g.has_zp || plan.sps != g.SPS || plan.m1 != m1) {
+            return fail(MNB_ERR_UNSUPPORTED, "item %d: a group needs one weight variant and one M class", i);
+        }
+        mnb::GemvParams &p = host[(size_t)i].p;
+        p.q_t = w->q_t;
+        p.s_t = w->s_t;
+        p.zp_t = (const uint8_t *)w->zp_t;
+        p.x = (const _Float16 *)it.x;
+        p.ldx = g.K;
+        p.kx = g.K;
+        p.M = it.M;
+        p.N = g.N;
+        p.ST = g.ST;
+        p.y = it.y;
+        p.y_f16 = it.y_type == MNB_F16;
+        p.accumulate = (it.flags & MNB_ACCUMULATE) ? 1 : 0;
+        host[(size_t)i].first_wg = (int32_t)wgs;
+        wgs += g.NT;
+        int waves = (g.ST + 3) / 4;
+        if (waves > 16) waves = 16;
+        if (waves > plan.waves) plan.waves = waves;
+    }
+    if (wgs > std::numeric_limits<int32_t>::max()) return fail(MNB_ERR_INVALID_ARGUMENT, "group too large");
+    std::vector<uint16_t> wg_item((size_t)wgs);
+    for (int32_t i = 0; i < count; ++i) {
+        const int32_t end = i + 1 < count ? host[(size_t)i + 1].first_wg : (int32_t)wgs;
+        for (int32_t b = host[(size_t)i].first_wg; b < end; ++b) wg_item[(size_t)b] = (uint16_t)i;
+    }
+    plan.count = count;
+    plan.total_wgs = (int32_t)wgs;
+    DeviceGuard guard(ctx->device);
+
+    // M == 1: static schedule for the persistent streaming kernel.  Units
+    // (item, n-tile) are assigned longest-first to the least loaded wave, cost
+    // = super-tiles + 1, and each wave keeps its units in group order.
+    std::vector<uint32_t> units;
+    std::vector<int32_t> wave_begin;
+    if (plan.m1) {
+        for (int32_t i = 0; i < count; ++i)
+            if (items[i].weight->g.NT > 65536)
+                return fail(MNB_ERR_UNSUPPORTED, "item %d: N=%d too large for a group", i, items[i].weight->g.N);
+        const int wpc = mnb::stream_kernel_waves_per_cu(plan.scale_f32, plan.has_zp, plan.sps);
+        const int64_t total_waves = (int64_t)ctx->cu_count * wpc;
+        plan.stream_wgs = (int32_t)(total_waves / mnb::kStreamWavesPerBlock);
+        const int64_t nwaves = (int64_t)plan.stream_wgs * mnb::kStreamWavesPerBlock;
+        std::vector<std::pair<int32_t, uint32_t>> order;   // (cost, code)
+        order.reserve((size_t)wgs);
+        for (int32_t i = 0; i < count; ++i) {
+            const WeightGeom &g = items[i].weight->g;
+            for (int32_t nt = 0; nt < g.NT; ++nt) order.emplace_back(g.ST + 1, ((uint32_t)i << 16) | (uint32_t)nt);
+        }
+        std::stable_sort(order.begin(), order.end(),
+                         [](const std::pair<int32_t, uint32_t> &a, const std::pair<int32_t, uint32_t> &b) { return a.first > b.first; });
+        typedef std::pair<int64_t, int32_t> Load;   // (cost, wave)
+        std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+        for (int32_t w = 0; w < (int32_t)nwaves; ++w) heap.push(Load(0, w));
+        std::vector<std::vector<uint32_t>> per((size_t)nwaves);
+        for (const auto &u : order) {
+            Load l = heap.top();
+            heap.pop();
+            per[(size_t)l.second].push_back(u.second);
+            l.first += u.first;
+            heap.push(l);
+        }
+        // per wave: first unit, number of super-tiles of its units; then the end
+        wave_begin.reserve(2 * (size_t)nwaves + 1);
+        units.reserve(order.size());
+        for (auto &v : per) {
+            std::sort(v.begin(), v.end());
+            int64_t jobs = 0;
+            for (uint32_t c : v) jobs += items[c >> 16].weight->g.ST;
+            if (jobs > std::numeric_limits<int32_t>::max()) return fail(MNB_ERR_INVALID_ARGUMENT, "group too large");
+            wave_begin.push_back((int32_t)units.size());
+            wave_begin.push_back((int32_t)jobs);
+            units.insert(units.end(), v.begin(), v.end());
+        }
+        wave_begin.push_back((int32_t)units.size());
+    }
+
+    hipError_t e;
+    auto release = [&]() {
+        if (plan.items) (void)hipFree(plan.items);
+        if (plan.wg_item) (void)hipFree(plan.wg_item);
+        if (plan.units) (void)hipFree(plan.units);
+        if (plan.wave_begin) (void)hipFree(plan.wave_begin);
+    };
+    if ((e = dev_alloc(&plan.items, host.size() * sizeof(mnb::GroupItem))) != hipSuccess ||
+        (e = dev_alloc(&plan.wg_item, wg_item.size() * sizeof(uint16_t))) != hipSuccess ||
+        (e = hipMemcpy(plan.items, host.data(), host.size() * sizeof(mnb::GroupItem), hipMemcpyHostToDevice)) != hipSuccess ||
+        (e = hipMemcpy(plan.wg_item, wg_item.data(), wg_item.size() * sizeof(uint16_t), hipMemcpyHostToDevice)) != hipSuccess ||
+        (plan.m1 && ((e = dev_alloc(&plan.units, units.size() * sizeof(uint32_t))) != hipSuccess ||
+                     (e = dev_alloc(&plan.wave_begin, wave_begin.size() * sizeof(int32_t))) != hipSuccess ||
+                     (e = hipMemcpy(plan.units, units.data(), units.size() * sizeof(uint32_t), hipMemcpyHostToDevice)) != hipSuccess ||
+                     (e = hipMemcpy(plan.wave_begin, wave_begin.data(), wave_begin.size() * sizeof(int32_t), hipMemcpyHostToDevice)) != hipSuccess))) {
+        release();
+        return hip_fail(e, "group");
+    }
+    mnb_group *grp = new mnb_group();
+    grp->ctx = ctx;
+    grp->plan = plan;
+    ctx->live_weights++;   // a group keeps its context alive like a weight does
+    *out = grp;
+    return ok();
+}
+
+int32_t mnb_group_run(mnb_context *ctx, const mnb_group *group, void *stream) {
+    if (!ctx || !group) return fail(MNB_ERR_INVALID_STATE, "Kernel not prepared");
+    if (group->ctx != ctx) return fail(MNB_ERR_INVALID_ARGUMENT, "group belongs to another context");
+    DeviceGuard guard(ctx->device);
+    hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    hipError_t e = group->plan.m1 ? mnb::launch_gemv_stream(group->plan, s) : mnb::launch_gemv_group(group->plan, s);
+    if (e != hipSuccess) return hip_fail(e, "matvec");
+    return ok();
+}
+
+int32_t mnb_group_destroy(mnb_group *group) {
+    if (!group) return ok();
+    DeviceGuard guard(group->ctx->device);
+    hipError_t first = hipStreamSynchronize(group->ctx->stream), e;
+    if ((e = hipFree(group->plan.items)) != hipSuccess && first == hipSuccess) first = e;
+    if ((e = hipFree(group->plan.wg_item)) != hipSuccess && first == hipSuccess) first = e;
+    if (group->plan.units && (e = hipFree(group->plan.units)) != hipSuccess && first == hipSuccess) first = e;
+    if (group->plan.wave_begin && (e = hipFree(group->plan.wave_begin)) != hipSuccess && first == hipSuccess) first = e;
+    group->ctx->live_weights--;
+    delete group;
+    if (first != hipSuccess) return hip_fail(first, "close");
     return ok();
 }
 

@@ -63,6 +63,14 @@ __device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
     return c;
 }
 
+// Load through the global address space: pointers read from memory are
+// generic to the compiler and would otherwise become flat loads, whose wait
+// counter is shared with LDS and forces full waits.
+template <typename T>
+__device__ __forceinline__ T gld(const T *p) {
+    return *(const __attribute__((address_space(1))) T *)p;
+}
+
 // The i-th nibble (low first) of a zero-point entry.
 __device__ __forceinline__ uint32_t zp_nibble(uint32_t zbits, int i) { return (zbits >> (4 * i)) & 0xFu; }
 
@@ -83,9 +91,46 @@ __device__ __forceinline__ void load_scales(const ScaleT *p, float (&s)[SPS]) {
 // Load one zero-point entry of ZB bytes.
 template <int ZB>
 __device__ __forceinline__ uint32_t load_zp(const uint8_t *p) {
-    if constexpr (ZB == 1) return *p;
-    else if constexpr (ZB == 2) return *(const uint16_t *)p;
-    else return *(const uint32_t *)p;
+    if constexpr (ZB == 1) return gld(p);
+    else if constexpr (ZB == 2) return gld((const uint16_t *)p);
+    else return gld((const uint32_t *)p);
+}
+
+template <bool F16>
+__device__ __forceinline__ void store_y(void *y, size_t idx, float v, bool accumulate) {
+    if constexpr (F16) {
+        __attribute__((address_space(1))) _Float16 *p = (__attribute__((address_space(1))) _Float16 *)y + idx;
+        if (accumulate) v += (float)*p;
+        *p = (_Float16)v;
+    } else {
+        __attribute__((address_space(1))) float *p = (__attribute__((address_space(1))) float *)y + idx;
+        if (accumulate) v += *p;
+        *p = v;
+    }
+}
+
+// Load the SPS scales of one row of one tile (SPS * sizeof(ScaleT) bytes,
+// naturally aligned in the tiled layout) with the widest vector load.
+template <typename ScaleT, int SPS>
+__device__ __forceinline__ void load_scale_row(const ScaleT *p, ScaleT (&s)[SPS]) {
+    constexpr int BYTES = SPS * (int)sizeof(ScaleT);
+    if constexpr (BYTES == 2) {
+        uint16_t v = gld((const uint16_t *)p);
+        __builtin_memcpy(&s, &v, 2);
+    } else if constexpr (BYTES == 4) {
+        uint32_t v = gld((const uint32_t *)p);
+        __builtin_memcpy(&s, &v, 4);
+    } else if constexpr (BYTES == 8) {
+        u32x2_t v = gld((const u32x2_t *)p);
+        __builtin_memcpy(&s, &v, 8);
+    } else if constexpr (BYTES == 16) {
+        u32x4_t v = gld((const u32x4_t *)p);
+        __builtin_memcpy(&s, &v, 16);
+    } else {
+        u32x4_t v0 = gld((const u32x4_t *)p), v1 = gld((const u32x4_t *)p + 1);
+        __builtin_memcpy(&s, &v0, 16);
+        __builtin_memcpy((char *)&s + 16, &v1, 16);
+    }
 }
 
 }  // namespace mnb

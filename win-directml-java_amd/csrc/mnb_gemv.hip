@@ -19,62 +19,17 @@
 
 namespace mnb {
 
-struct GemvParams {
-    const u32x4_t *q_t;
-    const void *s_t;
-    const uint8_t *zp_t;
-    const _Float16 *x;
-    int32_t ldx, kx, M, N, ST;
-    void *y;
-    int32_t y_f16, accumulate;
-};
-
-template <bool F16>
-__device__ __forceinline__ void store_y(void *y, size_t idx, float v, bool accumulate) {
-    if constexpr (F16) {
-        _Float16 *p = (_Float16 *)y + idx;
-        if (accumulate) v += (float)*p;
-        *p = (_Float16)v;
-    } else {
-        float *p = (float *)y + idx;
-        if (accumulate) v += *p;
-        *p = v;
-    }
-}
-
-// Load the SPS scales of one row of one tile (SPS * sizeof(ScaleT) bytes,
-// naturally aligned in the tiled layout) with the widest vector load.
-template <typename ScaleT, int SPS>
-__device__ __forceinline__ void load_scale_row(const ScaleT *p, ScaleT (&s)[SPS]) {
-    constexpr int BYTES = SPS * (int)sizeof(ScaleT);
-    if constexpr (BYTES == 2) {
-        uint16_t v = *(const uint16_t *)p;
-        __builtin_memcpy(&s, &v, 2);
-    } else if constexpr (BYTES == 4) {
-        uint32_t v = *(const uint32_t *)p;
-        __builtin_memcpy(&s, &v, 4);
-    } else if constexpr (BYTES == 8) {
-        u32x2_t v = *(const u32x2_t *)p;
-        __builtin_memcpy(&s, &v, 8);
-    } else if constexpr (BYTES == 16) {
-        u32x4_t v = *(const u32x4_t *)p;
-        __builtin_memcpy(&s, &v, 16);
-    } else {
-        u32x4_t v0 = ((const u32x4_t *)p)[0], v1 = ((const u32x4_t *)p)[1];
-        __builtin_memcpy(&s, &v0, 16);
-        __builtin_memcpy((char *)&s + 16, &v1, 16);
-    }
-}
-
 // M1: x has one row, staged once per workgroup in LDS (A operand = x
 // broadcast to all 16 MFMA rows).  !M1: up to 16 rows read from global
 // memory (rows >= M repeat row M-1 and their results are discarded).
 // STW: super-tiles per wave; all of a wave's weight, scale and zero-point
 // loads are issued before any arithmetic.
+// One workgroup computes the 16 outputs of n-tile `nt` (per activation row):
+// its W waves take chunks of STW super-tiles; waves beyond the chunk count
+// only take part in the final LDS reduction.
 template <typename ScaleT, bool HAS_ZP, bool M1, int SPS, int STW>
-__global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
+__device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, unsigned char *smem) {
     constexpr int ZB = SPS <= 2 ? 1 : SPS / 2;
-    extern __shared__ __align__(16) unsigned char smem[];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -83,11 +38,10 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
     // M1: each wave's slice of x (STW*128 halves) in a wave-private region
     _Float16 *xs = (_Float16 *)(smem + (size_t)W * 64 * sizeof(float4_t)) + wave * (STW * kTileK);
     const int r = lane & 15, gg = lane >> 4;
-    const int nt = blockIdx.x;
     const int nchunks = (p.ST + STW - 1) / STW;
 
     const size_t tile0 = (size_t)nt * p.ST;
-    const u32x4_t *qp = p.q_t + tile0 * 64 + lane;
+    const u32x4_t *qp = (const u32x4_t *)p.q_t + tile0 * 64 + lane;
     const ScaleT *sp = (const ScaleT *)p.s_t + (tile0 * kTileRows + r) * SPS;
     const uint8_t *zpp = HAS_ZP ? p.zp_t + (tile0 * kTileRows + r) * ZB : nullptr;
     const int m = M1 ? 0 : (r < p.M ? r : p.M - 1);
@@ -122,12 +76,8 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
         return (lane < STW * (kTileK / 8) && k < p.kx) ? v : zero4;
     };
 
-    u32x4_t xv = zero4;
-    if constexpr (M1) xv = load_x_slice(wave);
-    issue(wave);   // the host launches at most nchunks waves, so wave < nchunks
-    __builtin_amdgcn_sched_barrier(0);   // every load of the chunk is issued before any arithmetic
-
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    u32x4_t xv = zero4;
     auto compute_chunk = [&](int c) {
         if constexpr (M1) {
             // wave-private LDS: a wave's LDS accesses complete in order, no barrier needed
@@ -182,14 +132,19 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
         }
     };
 
-    // The first chunk is straight-line code after its loads; further chunks
-    // (K > 16 waves x STW x 128) loop.
-    compute_chunk(wave);
-    for (int c = wave + W; c < nchunks; c += W) {
-        if constexpr (M1) xv = load_x_slice(c);
-        issue(c);
-        __builtin_amdgcn_sched_barrier(0);
-        compute_chunk(c);
+    if (wave < nchunks) {
+        // The first chunk is straight-line code after its loads; further
+        // chunks (K > W x STW x 128) loop.
+        if constexpr (M1) xv = load_x_slice(wave);
+        issue(wave);
+        __builtin_amdgcn_sched_barrier(0);   // every load of the chunk is issued before any arithmetic
+        compute_chunk(wave);
+        for (int c = wave + W; c < nchunks; c += W) {
+            if constexpr (M1) xv = load_x_slice(c);
+            issue(c);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_chunk(c);
+        }
     }
 
     if (W > 1) {
@@ -225,6 +180,23 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
             }
         }
     }
+}
+
+template <typename ScaleT, bool HAS_ZP, bool M1, int SPS, int STW>
+__global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    gemv_tile<ScaleT, HAS_ZP, M1, SPS, STW>(p, blockIdx.x, smem);
+}
+
+// A group of independent projections in one launch: workgroup b computes
+// n-tile b - first_wg of item wg_item[b].
+template <typename ScaleT, bool HAS_ZP, bool M1, int SPS, int STW>
+__global__ __launch_bounds__(1024) void gemv_group_kernel(const GroupItem *__restrict__ items,
+                                                          const uint16_t *__restrict__ wg_item) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int it = wg_item[blockIdx.x];
+    const GemvParams p = items[it].p;
+    gemv_tile<ScaleT, HAS_ZP, M1, SPS, STW>(p, (int)blockIdx.x - items[it].first_wg, smem);
 }
 
 struct GemvLaunch {
@@ -294,6 +266,33 @@ hipError_t launch_gemv(const mnb_weight *w, const MatmulArgs &a, int32_t cu_coun
     L.block = dim3(64 * waves);
     L.lds = (size_t)waves * 64 * sizeof(float4_t) + (m1 ? (size_t)waves * L.stw * kTileK * 2 : 0);
     return g.scale_f32 ? gemv_zp<float>(g, L, p, m1, stream) : gemv_zp<_Float16>(g, L, p, m1, stream);
+}
+
+hipError_t launch_gemv_group(const GemvGroupPlan &g, hipStream_t stream) {
+    dim3 grid(g.total_wgs), block(64 * g.waves);
+    const size_t lds = (size_t)g.waves * 64 * sizeof(float4_t) + (g.m1 ? (size_t)g.waves * 4 * kTileK * 2 : 0);
+    const GroupItem *it = (const GroupItem *)g.items;
+    const uint16_t *wi = (const uint16_t *)g.wg_item;
+#define MNB_GROUP_LAUNCH(ST_, ZP_, M1_, SPS_)                                                                      \
+    hipLaunchKernelGGL((gemv_group_kernel<ST_, ZP_, M1_, SPS_, 4>), grid, block, lds, stream, it, wi)
+#define MNB_GROUP_SPS(ST_, ZP_, M1_)                              \
+    switch (g.sps) {                                              \
+        case 1: MNB_GROUP_LAUNCH(ST_, ZP_, M1_, 1); break;        \
+        case 2: MNB_GROUP_LAUNCH(ST_, ZP_, M1_, 2); break;        \
+        case 4: MNB_GROUP_LAUNCH(ST_, ZP_, M1_, 4); break;        \
+        case 8: MNB_GROUP_LAUNCH(ST_, ZP_, M1_, 8); break;        \
+        default: return hipErrorInvalidValue;                     \
+    }
+    if (g.scale_f32) {
+        if (g.has_zp) { if (g.m1) { MNB_GROUP_SPS(float, true, true) } else { MNB_GROUP_SPS(float, true, false) } }
+        else { if (g.m1) { MNB_GROUP_SPS(float, false, true) } else { MNB_GROUP_SPS(float, false, false) } }
+    } else {
+        if (g.has_zp) { if (g.m1) { MNB_GROUP_SPS(_Float16, true, true) } else { MNB_GROUP_SPS(_Float16, true, false) } }
+        else { if (g.m1) { MNB_GROUP_SPS(_Float16, false, true) } else { MNB_GROUP_SPS(_Float16, false, false) } }
+    }
+#undef MNB_GROUP_SPS
+#undef MNB_GROUP_LAUNCH
+    return hipGetLastError();
 }
 
 }  // namespace mnb

@@ -104,6 +104,41 @@ struct MatmulArgs {
     int32_t accumulate;
 };
 hipError_t launch_gemv(const mnb_weight *w, const MatmulArgs &a, int32_t cu_count, hipStream_t stream);
+
+// Kernel parameters of one skinny (M <= 16) product.
+struct GemvParams {
+    const void *q_t;
+    const void *s_t;
+    const uint8_t *zp_t;
+    const _Float16 *x;
+    int32_t ldx, kx, M, N, ST;
+    void *y;
+    int32_t y_f16, accumulate;
+};
+
+// One item of a group launch (device-resident array).
+struct GroupItem {
+    GemvParams p;
+    int32_t first_wg;   // first workgroup of this item in the group grid
+    int32_t pad;
+};
+
+// A recorded group of independent skinny products (all items share the
+// kernel variant: scale type, zero points, scales per super-tile, M == 1 or not).
+struct GemvGroupPlan {
+    void *items = nullptr;     // device GroupItem[count]
+    void *wg_item = nullptr;   // device uint16_t[total_wgs]: item of each workgroup (M > 1)
+    int32_t count = 0, total_wgs = 0, waves = 0;
+    int32_t scale_f32 = 0, has_zp = 0, sps = 0, m1 = 0;
+    // M == 1: persistent streaming schedule
+    void *units = nullptr;       // device uint32_t[U]: (item << 16) | n-tile, grouped by wave
+    void *wave_begin = nullptr;  // device int32_t[stream_wgs * 4 + 1]: first unit of each wave
+    int32_t stream_wgs = 0;
+};
+hipError_t launch_gemv_group(const GemvGroupPlan &g, hipStream_t stream);
+hipError_t launch_gemv_stream(const GemvGroupPlan &g, hipStream_t stream);
+int stream_kernel_waves_per_cu(int scale_f32, int has_zp, int sps);
+constexpr int kStreamWavesPerBlock = 4;
 hipError_t launch_gemm(const mnb_weight *w, const MatmulArgs &a, int32_t cu_count, hipStream_t stream);
 
 // largest M handled by the skinny (GEMV-style) kernel

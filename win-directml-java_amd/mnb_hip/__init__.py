@@ -50,7 +50,7 @@ EXPORTED_SYMBOLS = (
     "mnb_version", "mnb_last_error", "mnb_context_create", "mnb_context_destroy", "mnb_context_info",
     "mnb_weight_create", "mnb_weight_destroy", "mnb_weight_shape", "mnb_weight_device_bytes", "mnb_matmul",
     "mnb_dequantize", "mnb_supports_batch", "mnb_max_batch_rows", "mnb_device_alloc", "mnb_device_free",
-    "mnb_memcpy", "mnb_synchronize",
+    "mnb_memcpy", "mnb_synchronize", "mnb_group_create", "mnb_group_run", "mnb_group_destroy",
 )
 
 
@@ -76,6 +76,12 @@ class DeviceInfo(ctypes.Structure):
                 ("memory_bus_width", ctypes.c_int32), ("total_memory", ctypes.c_int64),
                 ("l2_bytes", ctypes.c_int32), ("lds_bytes_per_block", ctypes.c_int32),
                 ("wavefront_size", ctypes.c_int32), ("device", ctypes.c_int32)]
+
+
+class GroupItem(ctypes.Structure):
+    _fields_ = [("weight", ctypes.c_void_p), ("M", ctypes.c_int32), ("x", ctypes.c_void_p),
+                ("x_type", ctypes.c_int32), ("x_elems", ctypes.c_int64), ("y", ctypes.c_void_p),
+                ("y_type", ctypes.c_int32), ("y_elems", ctypes.c_int64), ("flags", ctypes.c_uint32)]
 
 
 _lib: Optional[ctypes.CDLL] = None
@@ -121,6 +127,9 @@ def load() -> ctypes.CDLL:
         "mnb_device_free": (i32, [vp, vp]),
         "mnb_memcpy": (i32, [vp, vp, vp, i64, i32]),
         "mnb_synchronize": (i32, [vp]),
+        "mnb_group_create": (i32, [vp, i32, ctypes.POINTER(GroupItem), ctypes.POINTER(vp)]),
+        "mnb_group_run": (i32, [vp, vp, vp]),
+        "mnb_group_destroy": (i32, [vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -280,6 +289,38 @@ class Weight:
         if self._h is not None:
             check(load().mnb_weight_destroy(self._h), "close")
             self._h = None
+
+
+class Group:
+    """Independent products recorded once and run as one launch (device tensors).
+
+    ``entries`` is a list of (Weight, x, y) with torch CUDA tensors; x is fp16
+    [M, K], y fp16 or fp32 [M, N], 1 <= M <= 16.  No item may read another
+    item's output (they may run concurrently)."""
+
+    def __init__(self, ctx: Context, entries, accumulate: bool = False):
+        L = load()
+        arr = (GroupItem * len(entries))()
+        for i, (w, x, y) in enumerate(entries):
+            M = x.numel() // w.K
+            arr[i] = GroupItem(w.handle.value, M, x.data_ptr(), _torch_dtype_code(x), x.numel(), y.data_ptr(),
+                               _torch_dtype_code(y), y.numel(), MNB_ACCUMULATE if accumulate else 0)
+        h = ctypes.c_void_p()
+        check(L.mnb_group_create(ctx.handle, len(entries), arr, ctypes.byref(h)), "group")
+        self._h = h
+        self.ctx = ctx
+        self._keep = entries
+
+    def run(self, stream=None) -> None:
+        if self._h is None:
+            raise IllegalStateException("group is closed")
+        check(load().mnb_group_run(self.ctx.handle, self._h, stream or None), "matvec")
+
+    def close(self) -> None:
+        if self._h is not None:
+            check(load().mnb_group_destroy(self._h), "close")
+            self._h = None
+            self._keep = None
 
 
 class MatMulNBitsKernel:
