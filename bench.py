@@ -51,9 +51,12 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-sweep", action="store_true")
+    p.add_argument("--eager", action="store_true", help="decode phase: launch directly instead of via a HIP graph")
+    p.add_argument("--phase", choices=("all", "decode"), default="all",
+                   help="decode: only the M=1 group launch and the copy calibration (for counter runs)")
     return p.parse_args()
 
 
@@ -146,6 +149,19 @@ def copy_bandwidth(torch, stream):
     return 2 * n / t / 1e9
 
 
+def measured_traffic(kernel_profile):
+    """HBM bytes per launch of the streaming kernel from its committed
+    rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated)."""
+    path = os.path.join(ROOT, "profiles", kernel_profile)
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch"):
+                return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(host, projs, seconds):
     """Oracle restatement of the reference CPU path on a bounded sample."""
     import mnb_oracle as orc
@@ -155,8 +171,8 @@ def cpu_baseline(host, projs, seconds):
     done_bytes = 0
     done = 0
     t_total = 0.0
-    while t_total < seconds and done < len(projs):
-        (name, layer, K, N), t = projs[done], host[done]
+    while t_total < seconds:
+        (name, layer, K, N), t = projs[done % len(projs)], host[done % len(projs)]
         s32 = orc.fp16_bits_to_fp32(t.scales_f16.view(np.uint16))
         z = np.full((N * t.kb + 1) // 2, 0x88, np.uint8)
         x = rng.standard_normal(K).astype(np.float16).astype(np.float32)
@@ -167,9 +183,9 @@ def cpu_baseline(host, projs, seconds):
         done_bytes += t.algorithmic_bytes(1)
         done += 1
     return {"value": round(done_bytes / t_total / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": "first %d of the %d decode-step projections at M=1 (%.2f GB), fp32 activations, "
-                      "8-lane FMA block dot, %d threads, %.1f s" % (done, len(projs), done_bytes / 1e9, threads,
-                                                                     t_total)}
+            "sample": "%d decode-step projections at M=1 in step order (%.2f GB of weights, %.2f steps), fp32 "
+                      "activations, 8-lane FMA block dot, %d threads, %.1f s" % (
+                          done, done_bytes / 1e9, done / len(projs), threads, t_total)}
 
 
 def main():
@@ -202,26 +218,48 @@ def main():
     gen = torch.Generator(device="cuda").manual_seed(5)
     xs = [torch.randn(K, device="cuda", generator=gen).half() for (_, _, K, _) in projs]
     ys = [torch.empty(N, device="cuda", dtype=torch.float16) for (_, _, _, N) in projs]
-    dec = Launcher(ctx, weights, xs, ys, 1, stream)
-    g_dec = capture(torch, dec, stream)
-    wall, gpu = time_graph(torch, g_dec, stream, args.steps, args.warmup)
-    value = bytes_step / wall / 1e9
-    log("decode step: %.1f us wall, %.1f us gpu, %.1f GB/s" % (wall * 1e6, gpu * 1e6, value))
-    # the same 129 projections recorded as one group launch (independent items)
+
+    # (1) headline: the 129 projections (each with its own activation, no
+    #     dependence between them) recorded once as a group and run as one
+    #     launch of the streaming kernel.
     grp = mnb_hip.Group(ctx, list(zip(weights, xs, ys)))
-    g_grp = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(stream):
-        grp.run(stream.cuda_stream)
-    torch.cuda.synchronize()
-    with torch.cuda.graph(g_grp, stream=stream):
-        grp.run(stream.cuda_stream)
-    wall_g, gpu_g = time_graph(torch, g_grp, stream, args.steps, args.warmup)
-    value_group = bytes_step / wall_g / 1e9
-    log("decode step as one group launch: %.1f us wall, %.1f GB/s" % (wall_g * 1e6, value_group))
+    if args.eager:
+        class _Direct:
+            def replay(self):
+                grp.run(stream.cuda_stream)
+        g_grp = _Direct()
+    else:
+        g_grp = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            grp.run(stream.cuda_stream)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g_grp, stream=stream):
+            grp.run(stream.cuda_stream)
+    wall, gpu = time_graph(torch, g_grp, stream, args.steps, args.warmup)
+    value = bytes_step / wall / 1e9
+    achieved_gbs = bytes_step / gpu / 1e9      # one launch per step: event time = launch duration
+    log("decode step as one group launch: %.1f us wall, %.1f us kernel, %.1f GB/s" % (wall * 1e6, gpu * 1e6, value))
     del g_grp
     grp.close()
+
+    if args.phase == "decode":
+        copy_gbs = copy_bandwidth(torch, stream)
+        print(json.dumps({"phase": "decode", "group_gbs": round(value, 2), "kernel_us": round(gpu * 1e6, 2),
+                          "bytes_per_step": bytes_step, "device_copy_gbs": round(copy_gbs, 1),
+                          "copy_bytes_per_launch": 2 << 30}), flush=True)
+        for w in weights:
+            w.close()
+        ctx.close()
+        return
+
+    # (2) the same projections as 129 separate launches in stream order (each
+    #     launch waits for the previous one, as in a dependent decode chain).
+    dec = Launcher(ctx, weights, xs, ys, 1, stream)
+    g_dec = capture(torch, dec, stream)
+    wall_seq, gpu_seq = time_graph(torch, g_dec, stream, args.steps, args.warmup)
+    log("decode step as 129 launches: %.1f us wall, %.1f GB/s" % (wall_seq * 1e6, bytes_step / wall_seq / 1e9))
+    del g_dec
     d1 = per_launch_times(torch, dec, stream)
-    achieved_gbs = bytes_step / d1.sum() / 1e9
     per_shape = {}
     for (name, layer, K, N), t, d in zip(projs, host, d1):
         e = per_shape.setdefault(name, {"K": K, "N": N, "bytes": t.algorithmic_bytes(1), "us": []})
@@ -230,8 +268,7 @@ def main():
         us = float(np.mean(e.pop("us")))
         e["avg_us"] = round(us, 3)
         e["gbs"] = round(e["bytes"] / us / 1e3, 1)
-    log("per-launch: " + json.dumps(per_shape))
-    del g_dec
+    log("per-launch (event brackets): " + json.dumps(per_shape))
 
     # ---------------- prefill, M = 512 (+ sweep) ----------------
     def prefill(M):
@@ -295,11 +332,21 @@ def main():
         "data": "synthetic (seeded random int4 weights, fp16 scales in [0.005,0.02], fp16 N(0,1) activations)",
         "config": {"workload": "phi3-mini int4 decode step: 32 x {qkv 3072->9216, o 3072->3072, "
                                "gate_up 3072->16384, down 8192->3072} + lm_head 3072->32064, M=1, bs=32, "
-                               "implicit zero point 8, HIP graph of 129 launches",
+                               "implicit zero point 8, each projection with its own activation; "
+                               "the 129 projections recorded as one group and run as one launch",
                    "M": 1, "block_size": BLOCK, "projections": len(projs), "bytes_per_step": bytes_step},
         "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "mnb::gemv_kernel (M=1)", "per_shape": per_shape},
+                     "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("gemv_stream_phi3_decode_step.md"),
+                     "traffic_source": "profiles/gemv_stream_phi3_decode_step.md (rocprofv3 FETCH_SIZE + WRITE_SIZE)",
+                     "kernel": "mnb::gemv_stream_kernel (one launch per step)",
+                     "avg_launch_us": round(gpu * 1e6, 2)},
+        "decode_step_sequential": {"gbs": round(bytes_step / wall_seq / 1e9, 2),
+                                   "ms_per_step": round(wall_seq * 1e3, 4),
+                                   "frac_hbm_peak": round(bytes_step / wall_seq / 1e9 / HBM_PEAK_GBS, 4),
+                                   "note": "the same 129 projections as 129 stream-ordered launches "
+                                           "(mnb::gemv_kernel, HIP graph)",
+                                   "per_shape": per_shape},
         "prefill_m512": {"tflops": round(tflops512, 2), "ms_per_step": round(wall512 * 1e3, 4),
                          "flops_per_step": flops512, "frac_fp16_peak": round(tflops512 / FP16_PEAK_TFLOPS, 4),
                          "roofline": {"bound": "mfma", "achieved": round(kernel_tflops512, 2),
@@ -307,9 +354,6 @@ def main():
                                       "frac": round(kernel_tflops512 / FP16_PEAK_TFLOPS, 4),
                                       "kernel": "mnb::gemm_kernel (M=512)"},
                          "sweep_tflops": sweep},
-        "decode_step_group": {"gbs": round(value_group, 2), "ms_per_step": round(wall_g * 1e3, 4),
-                              "frac_hbm_peak": round(value_group / HBM_PEAK_GBS, 4),
-                              "note": "same 129 projections as one recorded group launch (independent items)"},
         "device_copy_gbs": round(copy_gbs, 1),
         "cpu_baseline": cpu,
     }

@@ -14,7 +14,10 @@
 
 namespace mnb {
 
-constexpr int kStreamDepth = 4;      // tiles in flight per wave
+#ifndef MNB_STREAM_DEPTH
+#define MNB_STREAM_DEPTH 4
+#endif
+constexpr int kStreamDepth = MNB_STREAM_DEPTH;   // tiles in flight per wave
 constexpr int kStreamWaves = 4;      // waves per workgroup
 
 // Per-unit view of one item, resolved with uniform (scalar) loads.

@@ -25,7 +25,8 @@ from typing import Optional
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libmnb_hip.so")
+# MNB_HIP_LIBRARY points the binding at another build of the same library.
+LIB_PATH = os.environ.get("MNB_HIP_LIBRARY") or os.path.join(_HERE, "libmnb_hip.so")
 CONTRACT_TEST_PATH = os.path.join(_HERE, "mnb_contract_test")
 
 MNB_OK = 0
