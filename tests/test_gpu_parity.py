@@ -6,7 +6,8 @@ Bars (stated per test):
 * matmul: |y - y_oracle| <= 1e-3 * sqrt(K) * max|x| * max|w| (K = true K),
   plus one fp16 ulp of |y_oracle| when the output is fp16.
 * full-size shapes: the oracle on sampled output rows, and properties that
-  hold bit-for-bit (power-of-two scaling, row independence, M-tiling).
+  hold bit-for-bit (power-of-two scaling, row independence of the skinny
+  kernel, run-to-run determinism of the stream-K GEMM).
 """
 import os
 import subprocess
@@ -262,13 +263,21 @@ def test_rows_are_independent_in_skinny_kernel(ctx):
     w.close()
 
 
-def test_gemm_tiling_invariance_and_pow2_scaling(ctx):
+def test_gemm_determinism_tiling_and_pow2_scaling(ctx):
+    """The stream-K GEMM splits K over workgroups by the tile count, so a row's
+    summation order depends on M: rows of an M=512 product match an M=128
+    product of the same rows to the tolerance, and repeated calls with the
+    same M are bitwise identical (partials are summed in a fixed order)."""
     t = synth.make_weight(13, 3072, 3072, 32)
     w = upload(ctx, t)
     x16 = synth.make_x(14, 512, 3072)
     y = w.matmul(x16)
+    for _ in range(3):
+        assert np.array_equal(w.matmul(x16).view(np.uint32), y.view(np.uint32))
     y_part = w.matmul(np.ascontiguousarray(x16[128:256]))
-    assert np.array_equal(y[128:256].view(np.uint32), y_part.view(np.uint32))
+    tol = orc.tolerance(3072, x16.astype(np.float32),
+                        w.dequantize(np.float32))
+    assert np.abs(y[128:256] - y_part).max() <= tol
     y2 = w.matmul((x16.astype(np.float32) * 2).astype(np.float16))
     assert np.array_equal(y2.view(np.uint32), (y * 2).view(np.uint32))
     x1 = synth.make_x(15, 1, 3072)

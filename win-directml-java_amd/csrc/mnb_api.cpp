@@ -200,6 +200,8 @@ int32_t mnb_context_destroy(mnb_context *ctx) {
     if (ctx->stage_raw) note(hipFree(ctx->stage_raw));
     if (ctx->stage_x) note(hipFree(ctx->stage_x));
     if (ctx->stage_y) note(hipFree(ctx->stage_y));
+    if (ctx->sk_ws) note(hipFree(ctx->sk_ws));
+    if (ctx->sk_cnt) note(hipFree(ctx->sk_cnt));
     note(hipStreamDestroy(ctx->stream));
     delete ctx;
     if (first != hipSuccess) return hip_fail(first, "close");
@@ -366,6 +368,38 @@ int32_t mnb_supports_batch(const mnb_weight *w) { return w ? 1 : 0; }
 
 int32_t mnb_max_batch_rows(void) { return std::numeric_limits<int32_t>::max() / 2; }
 
+// M > 16: stream-K GEMM over one persistent workgroup per CU.  The partial
+// tile workspace (sized for one workgroup per CU) and the per-tile arrival
+// counters (at least 16384 tiles, e.g. M = 4096 x N = 1M) live in the context
+// and are allocated on first use, so later calls -- and graphs captured from
+// them -- keep the same buffers; new counters are zeroed once, and every
+// launch leaves them zero again.  The kernel addresses x and the weights with
+// 32-bit byte offsets: rows of x go in chunks of at most 2 GiB, and packed
+// weights of 4 GiB or more are refused.
+static hipError_t launch_prefill(mnb_context *ctx, const mnb_weight *w, const mnb::MatmulArgs &a, hipStream_t s) {
+    const mnb::WeightGeom &g = w->g;
+    if ((uint64_t)g.NT * (uint64_t)g.ST * mnb::kTileBytes >= ((uint64_t)1 << 32)) return hipErrorInvalidValue;
+    const int64_t chunk_rows = std::max<int64_t>(128, (((int64_t)1 << 31) / ((int64_t)a.ldx * 2)) / 128 * 128);
+    const int chunk = (int)std::min<int64_t>(a.M, chunk_rows);
+    hipError_t e = ensure(&ctx->sk_ws, &ctx->sk_ws_cap, mnb::sk_workspace_bytes(ctx->cu_count));
+    if (e != hipSuccess) return e;
+    const size_t cnt_bytes = (size_t)std::max(mnb::sk_tiles(chunk, g.NT), 16384) * sizeof(int32_t);
+    if (ctx->sk_cnt_cap < cnt_bytes || !ctx->sk_cnt) {
+        if ((e = ensure(&ctx->sk_cnt, &ctx->sk_cnt_cap, cnt_bytes)) != hipSuccess) return e;
+        if ((e = hipMemsetAsync(ctx->sk_cnt, 0, ctx->sk_cnt_cap, s)) != hipSuccess) return e;
+    }
+    const size_t y_row = (size_t)g.N * (a.y_type == MNB_F16 ? 2 : 4);
+    for (int m0 = 0; m0 < a.M; m0 += chunk) {
+        mnb::MatmulArgs c = a;
+        c.M = std::min(chunk, a.M - m0);
+        c.x = a.x + (size_t)m0 * a.ldx;
+        c.y = (unsigned char *)a.y + (size_t)m0 * y_row;
+        const int G = mnb::sk_grid(mnb::sk_tiles(c.M, g.NT), g.ST, ctx->cu_count);
+        if ((e = mnb::launch_gemm_sk(w, c, G, (float *)ctx->sk_ws, (int32_t *)ctx->sk_cnt, s)) != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 int32_t mnb_matmul(mnb_context *ctx, const mnb_weight *w, int32_t M, const void *x, int32_t x_type, int64_t x_elems,
                    void *y, int32_t y_type, int64_t y_elems, uint32_t flags, void *stream) {
     if (!ctx || !w) return fail(MNB_ERR_INVALID_STATE, "Kernel not prepared");
@@ -435,7 +469,7 @@ int32_t mnb_matmul(mnb_context *ctx, const mnb_weight *w, int32_t M, const void 
     a.y = yd;
     a.y_type = y_type;
     a.accumulate = (flags & MNB_ACCUMULATE) ? 1 : 0;
-    e = M <= mnb::kSkinnyMaxM ? mnb::launch_gemv(w, a, ctx->cu_count, s) : mnb::launch_gemm(w, a, ctx->cu_count, s);
+    e = M <= mnb::kSkinnyMaxM ? mnb::launch_gemv(w, a, ctx->cu_count, s) : launch_prefill(ctx, w, a, s);
     if (e != hipSuccess) return hip_fail(e, op);
 
     if (host) {

@@ -65,6 +65,11 @@ struct mnb_context {
     size_t stage_x_cap = 0;
     void *stage_y = nullptr;
     size_t stage_y_cap = 0;
+    // stream-K GEMM: partial tiles and per-tile arrival counters
+    void *sk_ws = nullptr;
+    size_t sk_ws_cap = 0;
+    void *sk_cnt = nullptr;
+    size_t sk_cnt_cap = 0;
     mnb_device_info info{};
 };
 
@@ -139,7 +144,18 @@ hipError_t launch_gemv_group(const GemvGroupPlan &g, hipStream_t stream);
 hipError_t launch_gemv_stream(const GemvGroupPlan &g, hipStream_t stream);
 int stream_kernel_waves_per_cu(int scale_f32, int has_zp, int sps);
 constexpr int kStreamWavesPerBlock = 4;
-hipError_t launch_gemm(const mnb_weight *w, const MatmulArgs &a, int32_t cu_count, hipStream_t stream);
+
+// Stream-K GEMM (M > 16): G persistent workgroups share the (tile, k-stage)
+// iterations; ws holds sk_workspace_bytes(G) of fp32 partial tiles, cnt one
+// arrival counter per tile (sk_tiles), zero before the first launch (the
+// kernel leaves them zero).
+size_t sk_workspace_bytes(int G);
+int sk_tiles(int M, int NT);
+// Workgroup count for T tiles of ST stages on cu_count CUs (a cost model:
+// whole tiles per workgroup when that is cheapest, else stream-K).
+int sk_grid(int T, int ST, int cu_count);
+hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, int32_t *cnt,
+                          hipStream_t stream);
 
 // largest M handled by the skinny (GEMV-style) kernel
 constexpr int kSkinnyMaxM = 16;
