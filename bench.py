@@ -54,9 +54,10 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-sweep", action="store_true")
-    p.add_argument("--eager", action="store_true", help="decode phase: launch directly instead of via a HIP graph")
-    p.add_argument("--phase", choices=("all", "decode"), default="all",
-                   help="decode: only the M=1 group launch and the copy calibration (for counter runs)")
+    p.add_argument("--eager", action="store_true", help="launch directly instead of via HIP graphs (counter runs)")
+    p.add_argument("--phase", choices=("all", "decode", "prefill"), default="all",
+                   help="decode: only the M=1 group launch and the copy calibration; prefill: only the "
+                        "M=512 launches (both for counter runs)")
     return p.parse_args()
 
 
@@ -100,9 +101,10 @@ def time_graph(torch, graph, stream, steps, warmup):
 
 
 def per_launch_times(torch, launcher, stream, reps=3):
-    """Kernel duration of every launch, from a HIP event pair around it.  The
-    stream is first held by a GPU sleep so that all launches are queued
-    before the first one starts (no host gaps inside a bracket)."""
+    """Kernel duration of every launch (mean over reps), from a HIP event pair
+    around it on the launch stream.  The stream is first held by a GPU sleep so
+    that all launches are queued before the first one starts (no host gaps
+    inside a bracket)."""
     n = len(launcher.calls)
     durs = np.zeros((reps, n))
     for r in range(reps):
@@ -116,7 +118,22 @@ def per_launch_times(torch, launcher, stream, reps=3):
                 evs[i][1].record(stream)
         torch.cuda.synchronize()
         durs[r] = [a.elapsed_time(b) / 1e3 for a, b in evs]
-    return durs.min(axis=0)
+    return durs.mean(axis=0)
+
+
+def group_launch_times(torch, grp, stream, reps=20):
+    """Duration of each of reps queued launches of a recorded group (HIP event
+    pairs on the launch stream, queued behind a GPU sleep)."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    with torch.cuda.stream(stream):
+        if hasattr(torch.cuda, "_sleep"):
+            torch.cuda._sleep(int(40e6))
+        for a, b in evs:
+            a.record(stream)
+            grp.run(stream.cuda_stream)
+            b.record(stream)
+    torch.cuda.synchronize()
+    return np.array([a.elapsed_time(b) / 1e3 for a, b in evs])
 
 
 def capture(torch, launcher, stream):
@@ -149,13 +166,13 @@ def copy_bandwidth(torch, stream):
     return 2 * n / t / 1e9
 
 
-def measured_traffic(kernel_profile):
-    """HBM bytes per launch of the streaming kernel from its committed
-    rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated)."""
+def measured_traffic(kernel_profile, key="traffic_bytes_per_launch"):
+    """HBM bytes of a kernel from its committed rocprofv3 counter summary
+    (FETCH_SIZE + WRITE_SIZE, copy-calibrated)."""
     path = os.path.join(ROOT, "profiles", kernel_profile)
     try:
         for line in open(path):
-            if line.startswith("traffic_bytes_per_launch"):
+            if line.startswith(key):
                 return int(line.split("=")[1])
     except OSError:
         pass
@@ -216,6 +233,43 @@ def main():
 
     # ---------------- decode step, M = 1 ----------------
     gen = torch.Generator(device="cuda").manual_seed(5)
+
+    # prefill-shaped products: the same 129 projections at M rows, one launch each
+    def prefill(M):
+        xs_m, ys_m = {}, []
+        for (_, _, K, N) in projs:
+            if K not in xs_m:
+                xs_m[K] = torch.randn(M, K, device="cuda", generator=gen).half()
+        xs_l = [xs_m[K] for (_, _, K, _) in projs]
+        ybuf = {}
+        for (_, _, K, N) in projs:
+            if N not in ybuf:
+                ybuf[N] = torch.empty(M, N, device="cuda", dtype=torch.float16)
+            ys_m.append(ybuf[N])
+        la = Launcher(ctx, weights, xs_l, ys_m, M, stream)
+        if args.eager:
+            class _Direct:
+                def replay(self):
+                    la.run()
+            g = _Direct()
+        else:
+            g = capture(torch, la, stream)
+        steps = max(3, args.steps // 4) if M >= 512 else args.steps
+        wall_m, gpu_m = time_graph(torch, g, stream, steps, 2)
+        flops = sum(2.0 * M * N * K for (_, _, K, N) in projs)
+        del g
+        return la, flops, wall_m, gpu_m
+
+
+    if args.phase == "prefill":
+        _, fl, w_m, _ = prefill(512)
+        print(json.dumps({"phase": "prefill", "M": 512, "tflops": round(fl / w_m / 1e12, 2),
+                          "us_per_step": round(w_m * 1e6, 1), "flops_per_step": fl}), flush=True)
+        for w in weights:
+            w.close()
+        ctx.close()
+        return
+
     xs = [torch.randn(K, device="cuda", generator=gen).half() for (_, _, K, _) in projs]
     ys = [torch.empty(N, device="cuda", dtype=torch.float16) for (_, _, _, N) in projs]
 
@@ -237,14 +291,16 @@ def main():
             grp.run(stream.cuda_stream)
     wall, gpu = time_graph(torch, g_grp, stream, args.steps, args.warmup)
     value = bytes_step / wall / 1e9
-    achieved_gbs = bytes_step / gpu / 1e9      # one launch per step: event time = launch duration
-    log("decode step as one group launch: %.1f us wall, %.1f us kernel, %.1f GB/s" % (wall * 1e6, gpu * 1e6, value))
     del g_grp
+    kern = group_launch_times(torch, grp, stream, reps=args.steps).mean()   # one launch per step
+    achieved_gbs = bytes_step / kern / 1e9
+    log("decode step as one group launch: %.1f us per step, %.1f us per launch (event brackets), %.1f GB/s" % (
+        wall * 1e6, kern * 1e6, value))
     grp.close()
 
     if args.phase == "decode":
         copy_gbs = copy_bandwidth(torch, stream)
-        print(json.dumps({"phase": "decode", "group_gbs": round(value, 2), "kernel_us": round(gpu * 1e6, 2),
+        print(json.dumps({"phase": "decode", "group_gbs": round(value, 2), "kernel_us": round(kern * 1e6, 2),
                           "bytes_per_step": bytes_step, "device_copy_gbs": round(copy_gbs, 1),
                           "copy_bytes_per_launch": 2 << 30}), flush=True)
         for w in weights:
@@ -271,31 +327,13 @@ def main():
     log("per-launch (event brackets): " + json.dumps(per_shape))
 
     # ---------------- prefill, M = 512 (+ sweep) ----------------
-    def prefill(M):
-        xs_m, ys_m = {}, []
-        for (_, _, K, N) in projs:
-            if K not in xs_m:
-                xs_m[K] = torch.randn(M, K, device="cuda", generator=gen).half()
-        xs_l = [xs_m[K] for (_, _, K, _) in projs]
-        ybuf = {}
-        for (_, _, K, N) in projs:
-            if N not in ybuf:
-                ybuf[N] = torch.empty(M, N, device="cuda", dtype=torch.float16)
-            ys_m.append(ybuf[N])
-        la = Launcher(ctx, weights, xs_l, ys_m, M, stream)
-        g = capture(torch, la, stream)
-        steps = max(3, args.steps // 4) if M >= 512 else args.steps
-        wall_m, gpu_m = time_graph(torch, g, stream, steps, 2)
-        flops = sum(2.0 * M * N * K for (_, _, K, N) in projs)
-        del g
-        return la, flops, wall_m, gpu_m
-
     la512, flops512, wall512, gpu512 = prefill(512)
     tflops512 = flops512 / wall512 / 1e12
-    d512 = per_launch_times(torch, la512, stream, reps=2)
-    kernel_tflops512 = flops512 / d512.sum() / 1e12
-    log("prefill M=512: %.1f us wall, %.1f TFLOP/s (kernel-time %.1f TFLOP/s)" % (
-        wall512 * 1e6, tflops512, kernel_tflops512))
+    # the graph runs the 129 launches back to back (no gaps between kernels),
+    # so the GPU time per replay is the summed kernel time of one step
+    kernel_tflops512 = flops512 / gpu512 / 1e12
+    log("prefill M=512: %.1f us per step, %.1f us GPU time, %.1f TFLOP/s (kernel time %.1f TFLOP/s)" % (
+        wall512 * 1e6, gpu512 * 1e6, tflops512, kernel_tflops512))
     del la512
     sweep = {}
     if not args.no_sweep:
@@ -340,7 +378,7 @@ def main():
                      "traffic": measured_traffic("gemv_stream_phi3_decode_step.md"),
                      "traffic_source": "profiles/gemv_stream_phi3_decode_step.md (rocprofv3 FETCH_SIZE + WRITE_SIZE)",
                      "kernel": "mnb::gemv_stream_kernel (one launch per step)",
-                     "avg_launch_us": round(gpu * 1e6, 2)},
+                     "avg_launch_us": round(kern * 1e6, 2)},
         "decode_step_sequential": {"gbs": round(bytes_step / wall_seq / 1e9, 2),
                                    "ms_per_step": round(wall_seq * 1e3, 4),
                                    "frac_hbm_peak": round(bytes_step / wall_seq / 1e9 / HBM_PEAK_GBS, 4),
@@ -352,7 +390,13 @@ def main():
                          "roofline": {"bound": "mfma", "achieved": round(kernel_tflops512, 2),
                                       "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                       "frac": round(kernel_tflops512 / FP16_PEAK_TFLOPS, 4),
-                                      "kernel": "mnb::gemm_kernel (M=512)"},
+                                      "kernel": "mnb::gemm_sk_kernel (M=512, one launch per projection)",
+                                      "avg_launch_us": round(gpu512 / len(projs) * 1e6, 2),
+                                      "traffic": measured_traffic("gemm_sk_phi3_prefill_m512.md",
+                                                                  "traffic_bytes_per_step"),
+                                      "traffic_unit": "HBM bytes per step (129 launches)",
+                                      "traffic_source": "profiles/gemm_sk_phi3_prefill_m512.md "
+                                                        "(rocprofv3 FETCH_SIZE + WRITE_SIZE)"},
                          "sweep_tflops": sweep},
         "device_copy_gbs": round(copy_gbs, 1),
         "cpu_baseline": cpu,
