@@ -51,6 +51,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                   help="untimed GPU work before the warm-up steps of each timed phase (clock ramp after idle)")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-sweep", action="store_true")
@@ -82,7 +84,30 @@ class Launcher:
                 raise mnb_hip.MnbError(rc, mnb_hip.last_error())
 
 
-def time_graph(torch, graph, stream, steps, warmup):
+SETTLE_MS = 200.0
+
+
+def settle(torch, graph, stream, ms):
+    """Untimed replays for about `ms` of GPU time before any warm-up step.
+    After an idle period the MI355X ramps its clocks for tens of milliseconds
+    (the decode launch then drifts from 363 to 510 us and back to ~375 us over
+    ~25 launches); measurements are taken on the settled chip."""
+    if ms <= 0:
+        return
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        graph.replay()
+    torch.cuda.synchronize()
+    one = max(time.perf_counter() - t0, 1e-5)
+    n = int(min(10000, max(1, ms * 1e-3 / one)))
+    with torch.cuda.stream(stream):
+        for _ in range(n):
+            graph.replay()
+    torch.cuda.synchronize()
+
+
+def time_graph(torch, graph, stream, steps, warmup, settle_ms=0.0):
+    settle(torch, graph, stream, settle_ms)
     with torch.cuda.stream(stream):
         for _ in range(warmup):
             graph.replay()
@@ -122,12 +147,12 @@ def per_launch_times(torch, launcher, stream, reps=3):
 
 
 def group_launch_times(torch, grp, stream, reps=20):
-    """Duration of each of reps queued launches of a recorded group (HIP event
-    pairs on the launch stream, queued behind a GPU sleep)."""
+    """Duration of each of reps back-to-back launches of a recorded group (HIP
+    event pairs on the launch stream).  Called right after the timed graph
+    replays, on the settled chip; a launch takes far longer than enqueuing
+    the next one, so no host gap falls inside a bracket."""
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
     with torch.cuda.stream(stream):
-        if hasattr(torch.cuda, "_sleep"):
-            torch.cuda._sleep(int(40e6))
         for a, b in evs:
             a.record(stream)
             grp.run(stream.cuda_stream)
@@ -255,7 +280,7 @@ def main():
         else:
             g = capture(torch, la, stream)
         steps = max(3, args.steps // 4) if M >= 512 else args.steps
-        wall_m, gpu_m = time_graph(torch, g, stream, steps, 2)
+        wall_m, gpu_m = time_graph(torch, g, stream, steps, 2, args.settle_ms)
         flops = sum(2.0 * M * N * K for (_, _, K, N) in projs)
         del g
         return la, flops, wall_m, gpu_m
@@ -289,7 +314,7 @@ def main():
         torch.cuda.synchronize()
         with torch.cuda.graph(g_grp, stream=stream):
             grp.run(stream.cuda_stream)
-    wall, gpu = time_graph(torch, g_grp, stream, args.steps, args.warmup)
+    wall, gpu = time_graph(torch, g_grp, stream, args.steps, args.warmup, args.settle_ms)
     value = bytes_step / wall / 1e9
     del g_grp
     kern = group_launch_times(torch, grp, stream, reps=args.steps).mean()   # one launch per step
@@ -312,7 +337,7 @@ def main():
     #     launch waits for the previous one, as in a dependent decode chain).
     dec = Launcher(ctx, weights, xs, ys, 1, stream)
     g_dec = capture(torch, dec, stream)
-    wall_seq, gpu_seq = time_graph(torch, g_dec, stream, args.steps, args.warmup)
+    wall_seq, gpu_seq = time_graph(torch, g_dec, stream, args.steps, args.warmup, args.settle_ms)
     log("decode step as 129 launches: %.1f us wall, %.1f GB/s" % (wall_seq * 1e6, bytes_step / wall_seq / 1e9))
     del g_dec
     d1 = per_launch_times(torch, dec, stream)
@@ -362,6 +387,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms": args.settle_ms,
         "ms_per_step": round(wall * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
