@@ -48,6 +48,7 @@ extern "C" {
 #define MNB_ERR_DEVICE 4
 #define MNB_ERR_NO_DEVICE 5
 #define MNB_ERR_UNSUPPORTED 6
+#define MNB_ERR_IO 7 /* weight-file errors: the reference's IOException */
 
 /* element types */
 #define MNB_F32 0
@@ -206,6 +207,95 @@ int32_t mnb_memcpy(mnb_context *ctx, void *dst, const void *src, int64_t bytes, 
 /* Wait for all work on the context's stream.  Replaces the fence wait
  * (MNK:1894-1901). */
 int32_t mnb_synchronize(mnb_context *ctx);
+
+/* ---------------------------------------------------------------------------
+ * Weight files.  A pack is a read-only memory mapping of a file that holds
+ * MatMulNBits weight triplets, with its directory parsed and checked:
+ *
+ *   MNB_PACK_PHI3   .wdmlpack whose manifest says architecture "phi3": one
+ *                   triplet per role ("layers.<l>.q_proj", ..., "lm_head"):
+ *                   <role>.qweight UINT8 dims [N, K, blockSize], <role>.scales
+ *                   FLOAT [N*kb], <role>.zeropoints UINT8 flat nibble stream
+ *                   (PRP:35-46,132-152; Phi3WdmlPackCompiler.java:236-264).
+ *   MNB_PACK_QWEN2  .wdmlpack whose model.architecture is "qwen2": the ONNX
+ *                   initializers stored in the payload plus the MatMulNBits
+ *                   nodes of the manifest's runtimeGraph (QWS:59-185).  A
+ *                   manifest-only package opens its source ONNX model instead
+ *                   (QWS:76-86) and reports MNB_PACK_ONNX.
+ *   MNB_PACK_ONNX   ONNX model; MatMulNBits inputs [A, B, scales, zero_points?]
+ *                   (Q2W:534-545); external data in model.onnx_data or
+ *                   model.onnx.data beside the model (QwenModelDirValidator.java:163-174).
+ *
+ * Weight names are the Phi-3 roles, or the first output of each MatMulNBits
+ * node in graph order.  A triplet is resolved as the reference loads it
+ * (Q2W:936-976, 986-1121; PRP:132-145): N = dims[0], blockSize = 2*dims[2],
+ * K = kb*blockSize for ONNX; fp16 scales are widened with the reference's
+ * fp16ToFp32 (P3W:665-683, including its subnormal rounding); zero points are
+ * normalized to the flat nibble stream; a missing zero-point tensor means
+ * every zero point is 8.  Failures return MNB_ERR_IO with the reference's
+ * IOException text (WdmlPackWriter.java:114-177,254-259; WdmlPackManifest.java:
+ * 108-123; WdmlPackReader.java:67-96; Q2W:936-976,1017-1048,2063-2131).
+ *   PRP = directml-inference/src/main/java/com/aresstack/windirectml/inference/phi3/Phi3RuntimePackage.java
+ *   QWS = directml-inference/src/main/java/com/aresstack/windirectml/inference/qwen/QwenWdmlPackModelSource.java
+ * A pack is immutable after mnb_pack_open: concurrent calls on it are safe.
+ */
+#define MNB_PACK_PHI3 1
+#define MNB_PACK_QWEN2 2
+#define MNB_PACK_ONNX 3
+
+typedef struct mnb_pack mnb_pack;
+typedef struct mnb_triplet_info {
+    int32_t N;
+    int32_t K;              /* kb * block_size, as the reference derives it */
+    int32_t block_size;
+    int32_t blocks_per_row; /* K / block_size for Phi-3 (P3W:51-60), dims[1] for ONNX */
+    int64_t q_bytes;        /* packed nibbles as stored */
+    int64_t scale_count;    /* fp32 scales after widening */
+    int64_t zp_bytes;       /* flat zero-point stream (the 0x88 fill when zp_implicit) */
+    int32_t zp_implicit;    /* 1: no zero-point tensor, every zero point is 8 (Q2W:1107-1112) */
+    int32_t scale_dtype;    /* ONNX element type of the stored scales: 1 FLOAT, 10 FLOAT16 */
+} mnb_triplet_info;
+
+/* Open and check a weight file.  Replaces Phi3RuntimePackage.open (PRP:35-46)
+ * with its runtimeTensorCatalog (WdmlPackReader.java:37-96), the Qwen package
+ * and ONNX sources (QWS:59-185; Q2W:495-545, 1809-1938) and their tensor type
+ * checks (Q2W:2063-2117).  A file named *.wdmlpack or starting with the bytes
+ * "WDMLPACK" is read as a package; any other file as an ONNX model. */
+int32_t mnb_pack_open(const char *path, mnb_pack **out);
+
+/* Unmap the file.  Weights created from the pack stay valid (they live in
+ * HBM); this is the release of the host copies (Q2W:1754-1785).  NULL is
+ * accepted. */
+int32_t mnb_pack_close(mnb_pack *pack);
+
+int32_t mnb_pack_kind(const mnb_pack *pack, int32_t *kind);
+int32_t mnb_pack_weight_count(const mnb_pack *pack, int32_t *count);
+
+/* Name of weight `index` (0-based, in file order), NUL-terminated into buf
+ * (truncated to cap-1 bytes); *length receives the full length. */
+int32_t mnb_pack_weight_name(const mnb_pack *pack, int32_t index, char *buf, int64_t cap, int64_t *length);
+
+/* First weight whose name contains both "layers.<layer>" and `projection`,
+ * the lookup of Qwen2Weights.loadQuantizedProjection (Q2W:800-815); fails with
+ * "Quantized weight not found for layer <l> <projection>". */
+int32_t mnb_pack_find_projection(const mnb_pack *pack, int32_t layer, const char *projection, char *buf, int64_t cap,
+                                 int64_t *length);
+
+/* Shape and sizes of one triplet, resolved as above. */
+int32_t mnb_pack_weight_info(const mnb_pack *pack, const char *name, mnb_triplet_info *out);
+
+/* Host copy of one resolved triplet: the reference's QuantizedWeight arrays
+ * (qWeight bytes, fp32 scales, flat zero points; P3W:51-110, Q2W:58-79).
+ * Buffers must hold info.q_bytes, info.scale_count and info.zp_bytes. */
+int32_t mnb_pack_read_weight(const mnb_pack *pack, const char *name, uint8_t *q, int64_t q_cap, float *scales,
+                             int64_t scale_cap, uint8_t *zp, int64_t zp_cap);
+
+/* Upload one triplet straight from the mapping to HBM: mnb_weight_create on
+ * the resolved triplet (no host copy of the packed nibbles is made).  The
+ * same call as constructing the reference's GPU kernel from the loaded
+ * QuantizedWeight (MNK:940-970).  A zero-point stream whose nibbles are all 8
+ * is uploaded as the implicit zero point (identical values). */
+int32_t mnb_pack_weight_create(mnb_context *ctx, const mnb_pack *pack, const char *name, mnb_weight **out);
 
 #ifdef __cplusplus
 }

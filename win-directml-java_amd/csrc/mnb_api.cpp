@@ -142,6 +142,11 @@ struct DeviceGuard {
 
 }  // namespace
 
+int32_t mnb::report(int32_t code, const char *message) {
+    g_last_error = message ? message : "";
+    return code;
+}
+
 extern "C" {
 
 int32_t mnb_version(void) { return MNB_ABI_VERSION; }

@@ -88,6 +88,9 @@ namespace mnb {
 // enqueue on `stream`; they return the launch status.
 
 // natural layout (device copies of the caller's tensors) -> tiled layout
+// Records `message` as this thread's mnb_last_error() text and returns `code`.
+int32_t report(int32_t code, const char *message);
+
 hipError_t launch_repack(const WeightGeom &g, const uint8_t *q_nat, const void *s_nat, const uint8_t *zp_flat,
                          void *q_t, void *s_t, void *zp_t, hipStream_t stream);
 

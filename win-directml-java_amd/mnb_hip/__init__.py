@@ -36,6 +36,7 @@ MNB_ERR_OUT_OF_MEMORY = 3
 MNB_ERR_DEVICE = 4
 MNB_ERR_NO_DEVICE = 5
 MNB_ERR_UNSUPPORTED = 6
+MNB_ERR_IO = 7
 
 MNB_F32 = 0
 MNB_F16 = 1
@@ -45,6 +46,7 @@ MNB_ZP_ROW_PADDED = 2
 MNB_HOST_MEMORY = 0x1
 MNB_ACCUMULATE = 0x2
 MNB_COPY_H2D, MNB_COPY_D2H, MNB_COPY_D2D = 0, 1, 2
+MNB_PACK_PHI3, MNB_PACK_QWEN2, MNB_PACK_ONNX = 1, 2, 3
 
 # Every symbol include/mnb.h declares.
 EXPORTED_SYMBOLS = (
@@ -52,6 +54,8 @@ EXPORTED_SYMBOLS = (
     "mnb_weight_create", "mnb_weight_destroy", "mnb_weight_shape", "mnb_weight_device_bytes", "mnb_matmul",
     "mnb_dequantize", "mnb_supports_batch", "mnb_max_batch_rows", "mnb_device_alloc", "mnb_device_free",
     "mnb_memcpy", "mnb_synchronize", "mnb_group_create", "mnb_group_run", "mnb_group_destroy",
+    "mnb_pack_open", "mnb_pack_close", "mnb_pack_kind", "mnb_pack_weight_count", "mnb_pack_weight_name",
+    "mnb_pack_find_projection", "mnb_pack_weight_info", "mnb_pack_read_weight", "mnb_pack_weight_create",
 )
 
 
@@ -71,12 +75,23 @@ class IllegalStateException(RuntimeError):
     code = MNB_ERR_INVALID_STATE
 
 
+class IOException(OSError):
+    """Weight-file failure: the reference's java.io.IOException, with its message."""
+    code = MNB_ERR_IO
+
+
 class DeviceInfo(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 64), ("arch", ctypes.c_char * 64), ("compute_units", ctypes.c_int32),
                 ("clock_khz", ctypes.c_int32), ("memory_clock_khz", ctypes.c_int32),
                 ("memory_bus_width", ctypes.c_int32), ("total_memory", ctypes.c_int64),
                 ("l2_bytes", ctypes.c_int32), ("lds_bytes_per_block", ctypes.c_int32),
                 ("wavefront_size", ctypes.c_int32), ("device", ctypes.c_int32)]
+
+
+class TripletInfo(ctypes.Structure):
+    _fields_ = [("N", ctypes.c_int32), ("K", ctypes.c_int32), ("block_size", ctypes.c_int32),
+                ("blocks_per_row", ctypes.c_int32), ("q_bytes", ctypes.c_int64), ("scale_count", ctypes.c_int64),
+                ("zp_bytes", ctypes.c_int64), ("zp_implicit", ctypes.c_int32), ("scale_dtype", ctypes.c_int32)]
 
 
 class GroupItem(ctypes.Structure):
@@ -131,6 +146,15 @@ def load() -> ctypes.CDLL:
         "mnb_group_create": (i32, [vp, i32, ctypes.POINTER(GroupItem), ctypes.POINTER(vp)]),
         "mnb_group_run": (i32, [vp, vp, vp]),
         "mnb_group_destroy": (i32, [vp]),
+        "mnb_pack_open": (i32, [ctypes.c_char_p, ctypes.POINTER(vp)]),
+        "mnb_pack_close": (i32, [vp]),
+        "mnb_pack_kind": (i32, [vp, ctypes.POINTER(i32)]),
+        "mnb_pack_weight_count": (i32, [vp, ctypes.POINTER(i32)]),
+        "mnb_pack_weight_name": (i32, [vp, i32, ctypes.c_char_p, i64, ctypes.POINTER(i64)]),
+        "mnb_pack_find_projection": (i32, [vp, i32, ctypes.c_char_p, ctypes.c_char_p, i64, ctypes.POINTER(i64)]),
+        "mnb_pack_weight_info": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(TripletInfo)]),
+        "mnb_pack_read_weight": (i32, [vp, ctypes.c_char_p, vp, i64, vp, i64, vp, i64]),
+        "mnb_pack_weight_create": (i32, [vp, vp, ctypes.c_char_p, ctypes.POINTER(vp)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -152,6 +176,8 @@ def check(rc: int, op: str = "call") -> None:
         raise IllegalArgumentException(msg)
     if rc == MNB_ERR_INVALID_STATE:
         raise IllegalStateException(msg)
+    if rc == MNB_ERR_IO:
+        raise IOException(msg)
     raise MnbError(rc, msg)
 
 
@@ -238,6 +264,16 @@ class Weight:
         self._h = h
         self.ctx = ctx
         self.N, self.K, self.block_size = N, K, block_size
+
+    @classmethod
+    def _adopt(cls, ctx: Context, h: ctypes.c_void_p) -> "Weight":
+        """Wrap a weight handle the library created (e.g. mnb_pack_weight_create)."""
+        w = cls.__new__(cls)
+        w._h, w.ctx = h, ctx
+        n, k, bs = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        check(load().mnb_weight_shape(h, ctypes.byref(n), ctypes.byref(k), ctypes.byref(bs)), "prepare")
+        w.N, w.K, w.block_size = n.value, k.value, bs.value
+        return w
 
     @property
     def handle(self):
@@ -405,3 +441,95 @@ class QuantizedWeightMatrix:
 
     def K(self) -> int:
         return self.kernel.K
+
+
+def _name_bytes(name: str) -> bytes:
+    """Tensor and weight names are byte strings in the files; names that are
+    not valid UTF-8 round-trip through surrogate escapes."""
+    return name.encode("utf-8", "surrogateescape")
+
+
+class Pack:
+    """An opened weight file: a .wdmlpack package (Phi-3 roles or a Qwen
+    runtimeGraph) or an ONNX model with MatMulNBits nodes (include/mnb.h,
+    mnb_pack_*).  Mirrors Phi3RuntimePackage.open/weights and the quantized
+    branch of Qwen2Weights loading: names are Phi-3 roles or MatMulNBits
+    output names; failures raise ``IOException`` with the reference's text."""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        check(load().mnb_pack_open(os.fsencode(path), ctypes.byref(h)), "open")
+        self._h = h
+        self.path = path
+
+    @property
+    def handle(self):
+        if self._h is None:
+            raise IllegalStateException("pack is closed")
+        return self._h
+
+    @property
+    def kind(self) -> int:
+        k = ctypes.c_int32()
+        check(load().mnb_pack_kind(self.handle, ctypes.byref(k)))
+        return k.value
+
+    def names(self) -> list:
+        L = load()
+        n = ctypes.c_int32()
+        check(L.mnb_pack_weight_count(self.handle, ctypes.byref(n)))
+        out = []
+        for i in range(n.value):
+            ln = ctypes.c_int64()
+            check(L.mnb_pack_weight_name(self.handle, i, None, 0, ctypes.byref(ln)))
+            buf = ctypes.create_string_buffer(ln.value + 1)
+            check(L.mnb_pack_weight_name(self.handle, i, buf, ln.value + 1, ctypes.byref(ln)))
+            out.append(buf.value.decode("utf-8", "surrogateescape"))
+        return out
+
+    def find_projection(self, layer: int, projection: str) -> str:
+        L = load()
+        ln = ctypes.c_int64()
+        check(L.mnb_pack_find_projection(self.handle, layer, _name_bytes(projection), None, 0, ctypes.byref(ln)))
+        buf = ctypes.create_string_buffer(ln.value + 1)
+        check(L.mnb_pack_find_projection(self.handle, layer, _name_bytes(projection), buf, ln.value + 1,
+                                         ctypes.byref(ln)))
+        return buf.value.decode("utf-8", "surrogateescape")
+
+    def info(self, name: str) -> TripletInfo:
+        i = TripletInfo()
+        check(load().mnb_pack_weight_info(self.handle, _name_bytes(name), ctypes.byref(i)))
+        return i
+
+    def read(self, name: str):
+        """(qWeight uint8, scales float32, zeroPoints uint8): the resolved triplet on the host."""
+        i = self.info(name)
+        q = np.empty(i.q_bytes, np.uint8)
+        s = np.empty(i.scale_count, np.float32)
+        z = np.empty(i.zp_bytes, np.uint8)
+        check(load().mnb_pack_read_weight(self.handle, _name_bytes(name), q.ctypes.data, q.size, s.ctypes.data, s.size,
+                                          z.ctypes.data if z.size else None, z.size))
+        return q, s, z
+
+    def weight(self, ctx: Context, name: str) -> Weight:
+        """Upload one triplet to HBM (mnb_pack_weight_create)."""
+        h = ctypes.c_void_p()
+        check(load().mnb_pack_weight_create(ctx.handle, self.handle, _name_bytes(name), ctypes.byref(h)), "prepare")
+        return Weight._adopt(ctx, h)
+
+    def close(self) -> None:
+        if self._h is not None:
+            check(load().mnb_pack_close(self._h))
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
