@@ -123,6 +123,22 @@ int32_t mnb_weight_create(mnb_context *ctx, int32_t N, int32_t K, int32_t block_
                           int64_t scale_count, const uint8_t *zero_points, int64_t zp_bytes, int32_t zp_layout,
                           uint32_t flags, mnb_weight **out);
 
+/* New weight whose rows are the rows of parts[0], then parts[1], ... (all
+ * created on ctx with the same K and block size), built on the device from
+ * the parts' resident buffers.  Replaces QwenGpuKernels.tryFuseQuantizedRowwise
+ * (directml-inference/.../qwen/QwenGpuKernels.java:243-315) and
+ * Phi3GpuKernels.createFusedQKV (directml-inference/.../phi3/Phi3GpuKernels.java:
+ * 114-137).  The fused weight equals the weight created from the concatenated
+ * triplet; the parts stay valid and independent of it.  Unlike the reference,
+ * any N_i works (zero points are stored per row on the device, so the
+ * byte-alignment condition and its FP32 fallback do not arise), and the Phi-3
+ * QKV stays int4 (the reference concatenates fp32 dequantized rows: the same
+ * values).  Parts may differ in scale type (fp16 widens to fp32 exactly) and
+ * in having zero points (implicit 8 where absent).  A part with another K or
+ * block size fails with "part i has K=.. blockSize=.. but expected K=..
+ * blockSize=..". */
+int32_t mnb_weight_fuse_rows(mnb_context *ctx, const mnb_weight *const *parts, int32_t count, mnb_weight **out);
+
 /* Free the weight's device buffers.  Replaces MatMulNBitsKernel.close()
  * (MNK:2740-2800).  NULL is accepted. */
 int32_t mnb_weight_destroy(mnb_weight *w);

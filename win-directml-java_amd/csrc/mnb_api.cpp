@@ -345,6 +345,70 @@ int32_t mnb_weight_create(mnb_context *ctx, int32_t N, int32_t K, int32_t block_
     return ok();
 }
 
+int32_t mnb_weight_fuse_rows(mnb_context *ctx, const mnb_weight *const *parts, int32_t count, mnb_weight **out) {
+    if (!out) return fail(MNB_ERR_INVALID_ARGUMENT, "out must not be null");
+    *out = nullptr;
+    if (!ctx) return fail(MNB_ERR_INVALID_STATE, "Kernel not prepared: no context");
+    if (!parts || count < 1) return fail(MNB_ERR_INVALID_ARGUMENT, "count=%d: at least one part is needed", count);
+    int64_t rows = 0;
+    bool any_f32 = false, any_zp = false;
+    for (int32_t i = 0; i < count; ++i) {
+        const mnb_weight *p = parts[i];
+        if (!p) return fail(MNB_ERR_INVALID_STATE, "Kernel not prepared: part %d", i);
+        if (p->ctx != ctx) return fail(MNB_ERR_INVALID_ARGUMENT, "part %d belongs to another context", i);
+        if (p->g.K != parts[0]->g.K || p->g.bs != parts[0]->g.bs)
+            return fail(MNB_ERR_INVALID_ARGUMENT, "part %d has K=%d blockSize=%d but expected K=%d blockSize=%d", i,
+                        p->g.K, p->g.bs, parts[0]->g.K, parts[0]->g.bs);
+        rows += p->g.N;
+        any_f32 |= p->g.scale_f32 != 0;
+        any_zp |= p->g.has_zp != 0;
+    }
+    if (rows > std::numeric_limits<int32_t>::max())
+        return fail(MNB_ERR_INVALID_ARGUMENT, "fused N=%lld exceeds the 32-bit row count", (long long)rows);
+    WeightGeom g = mnb::make_geom((int32_t)rows, parts[0]->g.K, parts[0]->g.bs);
+    g.scale_f32 = any_f32 ? 1 : 0;
+    g.has_zp = any_zp ? 1 : 0;
+
+    DeviceGuard guard(ctx->device);
+    mnb_weight *w = new mnb_weight();
+    w->ctx = ctx;
+    w->g = g;
+    const size_t tiles = (size_t)g.NT * g.ST;
+    const size_t q_t_bytes = tiles * mnb::kTileBytes;
+    const size_t s_t_bytes = tiles * mnb::kTileRows * g.SPS * (g.scale_f32 ? 4 : 2);
+    const size_t z_t_bytes = g.has_zp ? tiles * mnb::kTileRows * g.ZB : 0;
+    hipError_t e = hipSuccess;
+    if ((e = dev_alloc(&w->q_t, q_t_bytes)) != hipSuccess || (e = dev_alloc(&w->s_t, s_t_bytes)) != hipSuccess ||
+        (g.has_zp && (e = dev_alloc(&w->zp_t, z_t_bytes)) != hipSuccess) ||
+        (e = hipMemsetAsync(w->q_t, 0, q_t_bytes, ctx->stream)) != hipSuccess ||
+        (e = hipMemsetAsync(w->s_t, 0, s_t_bytes, ctx->stream)) != hipSuccess ||
+        (g.has_zp && (e = hipMemsetAsync(w->zp_t, 0, z_t_bytes, ctx->stream)) != hipSuccess)) {
+        if (w->q_t) (void)hipFree(w->q_t);
+        if (w->s_t) (void)hipFree(w->s_t);
+        if (w->zp_t) (void)hipFree(w->zp_t);
+        delete w;
+        return hip_fail(e, "prepare");
+    }
+    int32_t row0 = 0;
+    for (int32_t i = 0; i < count && e == hipSuccess; ++i) {
+        const mnb_weight *p = parts[i];
+        e = mnb::launch_copy_rows(p->g, p->q_t, p->s_t, p->zp_t, g, w->q_t, w->s_t, w->zp_t, row0, ctx->stream);
+        row0 += p->g.N;
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(w->q_t);
+        (void)hipFree(w->s_t);
+        if (w->zp_t) (void)hipFree(w->zp_t);
+        delete w;
+        return hip_fail(e, "prepare");
+    }
+    w->bytes = (int64_t)(q_t_bytes + s_t_bytes + z_t_bytes);
+    ctx->live_weights++;
+    *out = w;
+    return ok();
+}
+
 int32_t mnb_weight_destroy(mnb_weight *w) {
     if (!w) return ok();
     DeviceGuard guard(w->ctx->device);

@@ -87,12 +87,20 @@ namespace mnb {
 // Kernel launchers (defined in the .hip files).  All take device pointers and
 // enqueue on `stream`; they return the launch status.
 
-// natural layout (device copies of the caller's tensors) -> tiled layout
 // Records `message` as this thread's mnb_last_error() text and returns `code`.
 int32_t report(int32_t code, const char *message);
 
+// natural layout (device copies of the caller's tensors) -> tiled layout
 hipError_t launch_repack(const WeightGeom &g, const uint8_t *q_nat, const void *s_nat, const uint8_t *zp_flat,
                          void *q_t, void *s_t, void *zp_t, hipStream_t stream);
+
+// Copies the N_src rows of one tiled weight into rows [row0, row0 + N_src) of
+// another with the same K and block size (row fusion).  dst must be zero
+// beforehand.  Scales widen fp16 -> fp32 when dst keeps fp32 scales; a source
+// without zero points writes zero point 8 for its blocks < kb.
+hipError_t launch_copy_rows(const WeightGeom &src_g, const void *src_q, const void *src_s, const void *src_zp,
+                            const WeightGeom &dst_g, void *dst_q, void *dst_s, void *dst_zp, int32_t row0,
+                            hipStream_t stream);
 
 // x[M, K] (f16 or f32, row stride K) -> fp16 [M, ldx] with zeros in k in [K, ldx)
 hipError_t launch_stage_x(const void *x, int32_t x_type, int32_t M, int32_t K, int32_t ldx, _Float16 *out,

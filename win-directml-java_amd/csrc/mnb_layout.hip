@@ -133,6 +133,62 @@ hipError_t launch_repack(const WeightGeom &g, const uint8_t *q_nat, const void *
     return e;
 }
 
+// Row fusion: one thread per (source row, super-tile) moves that row's four
+// 16-byte lane chunks of packed nibbles, its SPS scales and its ZB zero-point
+// bytes to the destination row.  Both weights share K and the block size, so
+// ST, SPS and ZB agree; padding k, blocks >= kb and rows past the end stay as
+// the zeroed destination holds them.
+template <typename SrcS, typename DstS>
+__global__ void copy_rows_kernel(WeightGeom sg, const uint32_t *__restrict__ sq, const SrcS *__restrict__ ss,
+                                 const uint8_t *__restrict__ sz, WeightGeom dg, uint32_t *__restrict__ dq,
+                                 DstS *__restrict__ ds, uint8_t *__restrict__ dz, int32_t row0) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (size_t)sg.N * sg.ST) return;
+    const int st = (int)(e % sg.ST);
+    const int rs = (int)(e / sg.ST);
+    const int rd = row0 + rs;
+    const size_t ts = (size_t)(rs / kTileRows) * sg.ST + st;
+    const size_t td = (size_t)(rd / kTileRows) * dg.ST + st;
+    const int ls = rs % kTileRows, ld = rd % kTileRows;
+#pragma unroll
+    for (int gg = 0; gg < 4; ++gg)
+        *(u32x4_t *)(dq + (td * 64 + gg * 16 + ld) * 4) = *(const u32x4_t *)(sq + (ts * 64 + gg * 16 + ls) * 4);
+    for (int i = 0; i < sg.SPS; ++i)
+        ds[(td * kTileRows + ld) * dg.SPS + i] = (DstS)ss[(ts * kTileRows + ls) * sg.SPS + i];
+    if (!dz) return;
+    if (sz) {
+        for (int b = 0; b < sg.ZB; ++b) dz[(td * kTileRows + ld) * dg.ZB + b] = sz[(ts * kTileRows + ls) * sg.ZB + b];
+        return;
+    }
+    uint32_t bits = 0;  // implicit zero point 8 for the blocks the row holds
+    for (int i = 0; i < sg.SPS; ++i) {
+        const int blk = sg.bs >= kTileK ? (st * kTileK) / sg.bs : st * sg.SPS + i;
+        if (blk < sg.kb) bits |= 8u << (4 * i);
+    }
+    for (int b = 0; b < dg.ZB; ++b) dz[(td * kTileRows + ld) * dg.ZB + b] = (uint8_t)(bits >> (8 * b));
+}
+
+hipError_t launch_copy_rows(const WeightGeom &sg, const void *sq, const void *ss, const void *sz, const WeightGeom &dg,
+                            void *dq, void *ds, void *dz, int32_t row0, hipStream_t stream) {
+    const unsigned T = 256;
+    const size_t n = (size_t)sg.N * sg.ST;
+    if (n == 0) return hipSuccess;
+    const dim3 grid(blocks_for(n, T)), block(T);
+    if (!dg.scale_f32)
+        hipLaunchKernelGGL((copy_rows_kernel<_Float16, _Float16>), grid, block, 0, stream, sg, (const uint32_t *)sq,
+                           (const _Float16 *)ss, (const uint8_t *)sz, dg, (uint32_t *)dq, (_Float16 *)ds,
+                           (uint8_t *)dz, row0);
+    else if (sg.scale_f32)
+        hipLaunchKernelGGL((copy_rows_kernel<float, float>), grid, block, 0, stream, sg, (const uint32_t *)sq,
+                           (const float *)ss, (const uint8_t *)sz, dg, (uint32_t *)dq, (float *)ds, (uint8_t *)dz,
+                           row0);
+    else
+        hipLaunchKernelGGL((copy_rows_kernel<_Float16, float>), grid, block, 0, stream, sg, (const uint32_t *)sq,
+                           (const _Float16 *)ss, (const uint8_t *)sz, dg, (uint32_t *)dq, (float *)ds,
+                           (uint8_t *)dz, row0);
+    return hipGetLastError();
+}
+
 template <typename XT>
 __global__ void stage_x_kernel(const XT *__restrict__ x, int32_t M, int32_t K, int32_t ldx, _Float16 *__restrict__ out) {
     const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;

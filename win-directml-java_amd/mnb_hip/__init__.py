@@ -51,7 +51,7 @@ MNB_PACK_PHI3, MNB_PACK_QWEN2, MNB_PACK_ONNX = 1, 2, 3
 # Every symbol include/mnb.h declares.
 EXPORTED_SYMBOLS = (
     "mnb_version", "mnb_last_error", "mnb_context_create", "mnb_context_destroy", "mnb_context_info",
-    "mnb_weight_create", "mnb_weight_destroy", "mnb_weight_shape", "mnb_weight_device_bytes", "mnb_matmul",
+    "mnb_weight_create", "mnb_weight_fuse_rows", "mnb_weight_destroy", "mnb_weight_shape", "mnb_weight_device_bytes", "mnb_matmul",
     "mnb_dequantize", "mnb_supports_batch", "mnb_max_batch_rows", "mnb_device_alloc", "mnb_device_free",
     "mnb_memcpy", "mnb_synchronize", "mnb_group_create", "mnb_group_run", "mnb_group_destroy",
     "mnb_pack_open", "mnb_pack_close", "mnb_pack_kind", "mnb_pack_weight_count", "mnb_pack_weight_name",
@@ -132,6 +132,7 @@ def load() -> ctypes.CDLL:
         "mnb_context_info": (i32, [vp, ctypes.POINTER(DeviceInfo)]),
         "mnb_weight_create": (i32, [vp, i32, i32, i32, i32, vp, i64, vp, i32, i64, vp, i64, i32, u32,
                                     ctypes.POINTER(vp)]),
+        "mnb_weight_fuse_rows": (i32, [vp, ctypes.POINTER(vp), i32, ctypes.POINTER(vp)]),
         "mnb_weight_destroy": (i32, [vp]),
         "mnb_weight_shape": (i32, [vp, ctypes.POINTER(i32), ctypes.POINTER(i32), ctypes.POINTER(i32)]),
         "mnb_weight_device_bytes": (i64, [vp]),
@@ -274,6 +275,15 @@ class Weight:
         check(load().mnb_weight_shape(h, ctypes.byref(n), ctypes.byref(k), ctypes.byref(bs)), "prepare")
         w.N, w.K, w.block_size = n.value, k.value, bs.value
         return w
+
+    @classmethod
+    def fuse_rows(cls, ctx: Context, parts) -> "Weight":
+        """Rows of parts[0], then parts[1], ... in one new weight (mnb_weight_fuse_rows):
+        QwenGpuKernels.tryFuseQuantizedRowwise / Phi3GpuKernels.createFusedQKV."""
+        arr = (ctypes.c_void_p * len(parts))(*[p.handle for p in parts])
+        h = ctypes.c_void_p()
+        check(load().mnb_weight_fuse_rows(ctx.handle, arr, len(parts), ctypes.byref(h)), "prepare")
+        return cls._adopt(ctx, h)
 
     @property
     def handle(self):
