@@ -230,6 +230,46 @@ def cpu_baseline(host, projs, seconds):
                           done, done_bytes / 1e9, done / len(projs), threads, t_total)}
 
 
+def qwen_tied_lm_head(torch, mnb_hip, ctx, stream, args):
+    """Qwen2.5-0.5B tied lm_head: embed_tokens [151936, 896] (fp32, N(0, 0.02))
+    quantized on the device to int4 (bs 128, fp32 scales, zero points), then
+    the tall-skinny M=1 product timed per launch (HIP events on the launch
+    stream, back-to-back launches after an untimed settle)."""
+    V, H = 151936, 896
+    gen = torch.Generator(device="cuda").manual_seed(151936)
+    emb = torch.randn(V, H, device="cuda", generator=gen) * 0.02
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    w = mnb_hip.Weight.quantize(ctx, emb)
+    quant_ms = (time.perf_counter() - t0) * 1e3
+    del emb
+    x = torch.randn(H, device="cuda", generator=gen).half()
+    y = torch.empty(V, device="cuda", dtype=torch.float16)
+    la = Launcher(ctx, [w], [x], [y], 1, stream)
+    g = capture(torch, la, stream)
+    settle(torch, g, stream, args.settle_ms)
+    reps = 50
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    with torch.cuda.stream(stream):
+        for a, b in evs:
+            a.record(stream)
+            la.run()
+            b.record(stream)
+    torch.cuda.synchronize()
+    us = float(np.mean([a.elapsed_time(b) for a, b in evs[5:]])) * 1e3
+    kb = H // 128
+    nbytes = V * H // 2 + V * kb * 4 + (V * kb + 1) // 2 + H * 2 + V * 2
+    del g
+    w.close()
+    gbs = nbytes / us / 1e3
+    log("qwen tied lm_head: quantize %.2f ms, M=1 product %.2f us, %.1f GB/s" % (quant_ms, us, gbs))
+    return {"shape": [V, H], "block_size": 128, "quantize_ms_incl_alloc": round(quant_ms, 3),
+            "m1_avg_launch_us": round(us, 3), "m1_bytes_per_launch": nbytes, "m1_gbs": round(gbs, 1),
+            "m1_frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "kernel": "mnb::gemv_kernel (fp32 scales, zero points, bs 128)",
+            "note": "bytes = packed int4 + fp32 scales + zero points + fp16 x and y"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -373,6 +413,9 @@ def main():
 
     for w in weights:
         w.close()
+    del weights
+    torch.cuda.empty_cache()
+    qwen_head = qwen_tied_lm_head(torch, mnb_hip, ctx, stream, args)
     ctx.close()
 
     cpu = None
@@ -425,6 +468,7 @@ def main():
                                                         "(rocprofv3 FETCH_SIZE + WRITE_SIZE)"},
                          "sweep_tflops": sweep},
         "device_copy_gbs": round(copy_gbs, 1),
+        "qwen_tied_lm_head": qwen_head,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

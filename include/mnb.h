@@ -139,6 +139,29 @@ int32_t mnb_weight_create(mnb_context *ctx, int32_t N, int32_t K, int32_t block_
  * blockSize=..". */
 int32_t mnb_weight_fuse_rows(mnb_context *ctx, const mnb_weight *const *parts, int32_t count, mnb_weight **out);
 
+/* Quantize a dense matrix data[rows, cols] (row-major, MNB_F32 or MNB_F16)
+ * to an int4 weight on the device: asymmetric min/max uint4 per block of
+ * block_size columns with the reference's arithmetic, so the weight's bytes
+ * equal those of Qwen2Weights.quantizeDenseRowsToUInt4 (Q2W:1352-1422; the
+ * tied lm_head of Q2W:1329-1350).  block_size 0 picks the reference's choice,
+ * the largest of 128, 64, 32, 16 dividing cols (chooseTiedLmHeadBlockSize,
+ * Q2W:1339-1346); otherwise one of those four dividing cols.  fp16 data is
+ * widened exactly (pass fp32 for the reference's own fp16 widening).  The
+ * weight keeps fp32 scales and zero points.  flags: MNB_HOST_MEMORY when
+ * data is a host pointer (copied through a temporary device buffer); device
+ * data must be 16-byte aligned.  Synchronous on the context's stream. */
+int32_t mnb_weight_quantize(mnb_context *ctx, const void *data, int32_t data_type, int32_t rows, int32_t cols,
+                            int32_t block_size, uint32_t flags, mnb_weight **out);
+
+/* Host copy of a resident weight as the reference's arrays: q [N, kb,
+ * bs/2] (q_cap >= N*kb*bs/2), fp32 scales [N*kb], flat zero points
+ * ((N*kb+1)/2 bytes; the 0x88 fill when the weight has the implicit zero
+ * point).  The accessors QuantizedWeight.qWeight()/scales()/zeroPoints()
+ * (P3W:83-110) for weights that exist only on the device (fused, quantized
+ * on the device, loaded from a file). */
+int32_t mnb_weight_read(mnb_context *ctx, const mnb_weight *w, uint8_t *q, int64_t q_cap, float *scales,
+                        int64_t scale_cap, uint8_t *zero_points, int64_t zp_cap);
+
 /* Free the weight's device buffers.  Replaces MatMulNBitsKernel.close()
  * (MNK:2740-2800).  NULL is accepted. */
 int32_t mnb_weight_destroy(mnb_weight *w);

@@ -409,6 +409,106 @@ int32_t mnb_weight_fuse_rows(mnb_context *ctx, const mnb_weight *const *parts, i
     return ok();
 }
 
+int32_t mnb_weight_quantize(mnb_context *ctx, const void *data, int32_t data_type, int32_t rows, int32_t cols,
+                            int32_t block_size, uint32_t flags, mnb_weight **out) {
+    if (!out) return fail(MNB_ERR_INVALID_ARGUMENT, "out must not be null");
+    *out = nullptr;
+    if (!ctx) return fail(MNB_ERR_INVALID_STATE, "Kernel not prepared: no context");
+    if (flags & ~MNB_HOST_MEMORY) return fail(MNB_ERR_INVALID_ARGUMENT, "unknown flags 0x%x", flags);
+    if (!data) return fail(MNB_ERR_INVALID_ARGUMENT, "data must not be null");
+    if (data_type != MNB_F16 && data_type != MNB_F32)
+        return fail(MNB_ERR_INVALID_ARGUMENT, "data_type=%d must be MNB_F16 or MNB_F32", data_type);
+    if (rows < 1 || cols < 1) return fail(MNB_ERR_INVALID_ARGUMENT, "rows=%d and cols=%d must be positive", rows, cols);
+    if (block_size == 0) {  // chooseTiedLmHeadBlockSize (Qwen2Weights.java:1339-1346)
+        for (int c : {128, 64, 32, 16})
+            if (cols % c == 0) {
+                block_size = c;
+                break;
+            }
+        if (block_size == 0)
+            return fail(MNB_ERR_INVALID_ARGUMENT, "Cannot runtime-quantize: hidden size %d is not block-aligned", cols);
+    }
+    if (block_size != 16 && block_size != 32 && block_size != 64 && block_size != 128)
+        return fail(MNB_ERR_INVALID_ARGUMENT, "block_size=%d must be 16, 32, 64 or 128", block_size);
+    if (cols % block_size)
+        return fail(MNB_ERR_INVALID_ARGUMENT, "cols=%d is not a multiple of block_size=%d", cols, block_size);
+    if (!(flags & MNB_HOST_MEMORY) && ((uintptr_t)data & 15))
+        return fail(MNB_ERR_INVALID_ARGUMENT, "device data must be 16-byte aligned");
+    WeightGeom g = mnb::make_geom(rows, cols, block_size);
+    g.scale_f32 = 1;
+    g.has_zp = 1;
+
+    DeviceGuard guard(ctx->device);
+    const size_t data_bytes = (size_t)rows * cols * dtype_size(data_type);
+    void *staged = nullptr;
+    hipError_t e = hipSuccess;
+    if (flags & MNB_HOST_MEMORY) {
+        if ((e = dev_alloc(&staged, data_bytes)) != hipSuccess) return hip_fail(e, "prepare");
+        if ((e = hipMemcpyAsync(staged, data, data_bytes, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess) {
+            (void)hipFree(staged);
+            return hip_fail(e, "prepare");
+        }
+    }
+    mnb_weight *w = new mnb_weight();
+    w->ctx = ctx;
+    w->g = g;
+    const size_t tiles = (size_t)g.NT * g.ST;
+    const size_t q_t_bytes = tiles * mnb::kTileBytes;
+    const size_t s_t_bytes = tiles * mnb::kTileRows * g.SPS * 4;
+    const size_t z_t_bytes = tiles * mnb::kTileRows * g.ZB;
+    if ((e = dev_alloc(&w->q_t, q_t_bytes)) != hipSuccess || (e = dev_alloc(&w->s_t, s_t_bytes)) != hipSuccess ||
+        (e = dev_alloc(&w->zp_t, z_t_bytes)) != hipSuccess ||
+        (e = mnb::launch_quantize(g, staged ? staged : data, data_type, w->q_t, (float *)w->s_t,
+                                  (uint8_t *)w->zp_t, ctx->stream)) != hipSuccess ||
+        (e = hipStreamSynchronize(ctx->stream)) != hipSuccess) {
+        if (staged) (void)hipFree(staged);
+        if (w->q_t) (void)hipFree(w->q_t);
+        if (w->s_t) (void)hipFree(w->s_t);
+        if (w->zp_t) (void)hipFree(w->zp_t);
+        delete w;
+        return hip_fail(e, "prepare");
+    }
+    if (staged) (void)hipFree(staged);
+    w->bytes = (int64_t)(q_t_bytes + s_t_bytes + z_t_bytes);
+    ctx->live_weights++;
+    *out = w;
+    return ok();
+}
+
+int32_t mnb_weight_read(mnb_context *ctx, const mnb_weight *w, uint8_t *q, int64_t q_cap, float *scales,
+                        int64_t scale_cap, uint8_t *zero_points, int64_t zp_cap) {
+    if (!ctx || !w) return fail(MNB_ERR_INVALID_STATE, "Kernel not prepared");
+    if (w->ctx != ctx) return fail(MNB_ERR_INVALID_ARGUMENT, "weight belongs to another context");
+    const WeightGeom &g = w->g;
+    const int64_t blocks = (int64_t)g.N * g.kb, q_bytes = (int64_t)g.N * g.Kpad / 2, zp_bytes = (blocks + 1) / 2;
+    if (!q || !scales || !zero_points) return fail(MNB_ERR_INVALID_ARGUMENT, "q, scales and zero_points must not be null");
+    if (q_cap < q_bytes || scale_cap < blocks || zp_cap < zp_bytes)
+        return fail(MNB_ERR_INVALID_ARGUMENT, "buffers too small: need q %lld bytes, %lld scales, %lld zero-point bytes",
+                    (long long)q_bytes, (long long)blocks, (long long)zp_bytes);
+    DeviceGuard guard(ctx->device);
+    void *dq = nullptr, *ds = nullptr, *dz = nullptr;
+    hipError_t e = hipSuccess;
+    std::vector<uint8_t> zb((size_t)blocks);
+    if ((e = dev_alloc(&dq, (size_t)q_bytes)) == hipSuccess && (e = dev_alloc(&ds, (size_t)blocks * 4)) == hipSuccess &&
+        (e = dev_alloc(&dz, (size_t)blocks)) == hipSuccess &&
+        (e = mnb::launch_unpack(w, (uint8_t *)dq, (float *)ds, (uint8_t *)dz, ctx->stream)) == hipSuccess &&
+        (e = hipMemcpyAsync(q, dq, (size_t)q_bytes, hipMemcpyDeviceToHost, ctx->stream)) == hipSuccess &&
+        (e = hipMemcpyAsync(scales, ds, (size_t)blocks * 4, hipMemcpyDeviceToHost, ctx->stream)) == hipSuccess &&
+        (e = hipMemcpyAsync(zb.data(), dz, (size_t)blocks, hipMemcpyDeviceToHost, ctx->stream)) == hipSuccess)
+        e = hipStreamSynchronize(ctx->stream);
+    if (dq) (void)hipFree(dq);
+    if (ds) (void)hipFree(ds);
+    if (dz) (void)hipFree(dz);
+    if (e != hipSuccess) return hip_fail(e, "read");
+    if (!g.has_zp) {  // createDefaultZeroPoints: every byte 0x88, the unused last nibble included
+        memset(zero_points, 0x88, (size_t)zp_bytes);
+        return ok();
+    }
+    memset(zero_points, 0, (size_t)zp_bytes);
+    for (int64_t i = 0; i < blocks; ++i) zero_points[i / 2] |= (uint8_t)((zb[(size_t)i] & 0xF) << (4 * (i & 1)));
+    return ok();
+}
+
 int32_t mnb_weight_destroy(mnb_weight *w) {
     if (!w) return ok();
     DeviceGuard guard(w->ctx->device);

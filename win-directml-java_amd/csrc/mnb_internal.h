@@ -102,6 +102,16 @@ hipError_t launch_copy_rows(const WeightGeom &src_g, const void *src_q, const vo
                             const WeightGeom &dst_g, void *dst_q, void *dst_s, void *dst_zp, int32_t row0,
                             hipStream_t stream);
 
+// data[N, K] (f32 or f16, row stride K, K a multiple of g.bs, g.bs in
+// {16, 32, 64, 128}) -> tiled weight with fp32 scales and zero points: the
+// reference's per-block min/max uint4 quantizer.
+hipError_t launch_quantize(const WeightGeom &g, const void *data, int32_t data_type, void *q_t, float *s_t,
+                           uint8_t *zp_t, hipStream_t stream);
+
+// tiled weight -> q [N, Kpad/2] natural packing, fp32 scales [N*kb], one zero
+// point per block [N*kb] (8 where the weight has the implicit zero point)
+hipError_t launch_unpack(const mnb_weight *w, uint8_t *q_nat, float *s_nat, uint8_t *zp_blocks, hipStream_t stream);
+
 // x[M, K] (f16 or f32, row stride K) -> fp16 [M, ldx] with zeros in k in [K, ldx)
 hipError_t launch_stage_x(const void *x, int32_t x_type, int32_t M, int32_t K, int32_t ldx, _Float16 *out,
                           hipStream_t stream);

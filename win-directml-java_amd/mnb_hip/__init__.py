@@ -51,7 +51,7 @@ MNB_PACK_PHI3, MNB_PACK_QWEN2, MNB_PACK_ONNX = 1, 2, 3
 # Every symbol include/mnb.h declares.
 EXPORTED_SYMBOLS = (
     "mnb_version", "mnb_last_error", "mnb_context_create", "mnb_context_destroy", "mnb_context_info",
-    "mnb_weight_create", "mnb_weight_fuse_rows", "mnb_weight_destroy", "mnb_weight_shape", "mnb_weight_device_bytes", "mnb_matmul",
+    "mnb_weight_create", "mnb_weight_fuse_rows", "mnb_weight_quantize", "mnb_weight_read", "mnb_weight_destroy", "mnb_weight_shape", "mnb_weight_device_bytes", "mnb_matmul",
     "mnb_dequantize", "mnb_supports_batch", "mnb_max_batch_rows", "mnb_device_alloc", "mnb_device_free",
     "mnb_memcpy", "mnb_synchronize", "mnb_group_create", "mnb_group_run", "mnb_group_destroy",
     "mnb_pack_open", "mnb_pack_close", "mnb_pack_kind", "mnb_pack_weight_count", "mnb_pack_weight_name",
@@ -133,6 +133,8 @@ def load() -> ctypes.CDLL:
         "mnb_weight_create": (i32, [vp, i32, i32, i32, i32, vp, i64, vp, i32, i64, vp, i64, i32, u32,
                                     ctypes.POINTER(vp)]),
         "mnb_weight_fuse_rows": (i32, [vp, ctypes.POINTER(vp), i32, ctypes.POINTER(vp)]),
+        "mnb_weight_quantize": (i32, [vp, vp, i32, i32, i32, i32, u32, ctypes.POINTER(vp)]),
+        "mnb_weight_read": (i32, [vp, vp, vp, i64, vp, i64, vp, i64]),
         "mnb_weight_destroy": (i32, [vp]),
         "mnb_weight_shape": (i32, [vp, ctypes.POINTER(i32), ctypes.POINTER(i32), ctypes.POINTER(i32)]),
         "mnb_weight_device_bytes": (i64, [vp]),
@@ -284,6 +286,36 @@ class Weight:
         h = ctypes.c_void_p()
         check(load().mnb_weight_fuse_rows(ctx.handle, arr, len(parts), ctypes.byref(h)), "prepare")
         return cls._adopt(ctx, h)
+
+    @classmethod
+    def quantize(cls, ctx: Context, data, block_size: int = 0, rows: Optional[int] = None,
+                 cols: Optional[int] = None) -> "Weight":
+        """Dense [rows, cols] -> int4 weight on the device (mnb_weight_quantize):
+        Qwen2Weights.quantizeDenseRowsToUInt4; block_size 0 = the reference's choice.
+        numpy data is a host array; a torch CUDA tensor is used in place."""
+        L = load()
+        h = ctypes.c_void_p()
+        if _is_torch(data):
+            rows, cols = (rows, cols) if rows is not None else tuple(data.shape)
+            check(L.mnb_weight_quantize(ctx.handle, data.data_ptr(), _torch_dtype_code(data), rows, cols, block_size,
+                                        0, ctypes.byref(h)), "prepare")
+        else:
+            a = np.ascontiguousarray(data)
+            rows, cols = (rows, cols) if rows is not None else a.shape
+            check(L.mnb_weight_quantize(ctx.handle, a.ctypes.data, _dtype_code(a.dtype), rows, cols, block_size,
+                                        MNB_HOST_MEMORY, ctypes.byref(h)), "prepare")
+        return cls._adopt(ctx, h)
+
+    def read(self):
+        """(qWeight uint8 [N*kb*bs/2], scales float32 [N*kb], zeroPoints uint8 flat): the
+        reference's QuantizedWeight arrays of this resident weight (mnb_weight_read)."""
+        kb = -(-self.K // self.block_size)
+        q = np.empty(self.N * kb * self.block_size // 2, np.uint8)
+        s = np.empty(self.N * kb, np.float32)
+        z = np.empty((self.N * kb + 1) // 2, np.uint8)
+        check(load().mnb_weight_read(self.ctx.handle, self.handle, q.ctypes.data, q.size, s.ctypes.data, s.size,
+                                     z.ctypes.data, z.size), "read")
+        return q, s, z
 
     @property
     def handle(self):
