@@ -287,6 +287,37 @@ def test_gemm_determinism_tiling_and_pow2_scaling(ctx):
     w.close()
 
 
+@pytest.mark.parametrize("M,K,N", [(200, 3072, 1000), (300, 4096, 1001), (130, 8192, 3072)])
+def test_gemm_split_tiles_tails_and_outputs(ctx, M, K, N):
+    """Few tiles, so stream-K splits them across workgroups and the partial
+    tiles go through the reduce kernel.  M and N tails (N % 4 != 0 falls back
+    to per-element stores), fp16 and fp32 outputs, y += and a y that is not
+    aligned for 4-element stores: all within the tolerance of the oracle,
+    bitwise repeatable, and y += equal to y0 + y."""
+    import torch
+    t = synth.make_weight(50 + M, N, K, 32, with_zp=True)
+    w = upload(ctx, t)
+    x16 = synth.make_x(51 + M, M, K)
+    y_ref, wmax = oracle_matmul(t, x16)
+    y32 = w.matmul(x16)
+    assert_parity(y32, y_ref, x16, t, wmax, False, "split f32 M=%d K=%d N=%d" % (M, K, N))
+    assert np.array_equal(w.matmul(x16).view(np.uint32), y32.view(np.uint32))
+    y16 = w.matmul(x16, out_dtype=np.float16)
+    assert np.array_equal(y16.view(np.uint16), y32.astype(np.float16).view(np.uint16))
+    y0 = np.random.default_rng(M).standard_normal((M, N)).astype(np.float32)
+    acc = w.matmul(x16, y=y0.copy(), accumulate=True)
+    assert np.array_equal(acc.view(np.uint32), (y0 + y32).view(np.uint32))
+    # device output one element past an aligned address: per-element stores
+    xd = torch.from_numpy(x16).cuda()
+    buf = torch.zeros(M * N + 1, dtype=torch.float32, device="cuda")
+    yd = buf[1:]
+    w.matmul(xd, yd)
+    torch.cuda.synchronize()
+    assert np.array_equal(yd.cpu().numpy().reshape(M, N).view(np.uint32), y32.view(np.uint32))
+    assert float(buf[0].item()) == 0.0
+    w.close()
+
+
 def test_accumulate_and_dtypes_and_zp_layouts(ctx):
     t = synth.make_weight(21, 1536, 576, 64, with_zp=True)
     w_rp = upload(ctx, t)

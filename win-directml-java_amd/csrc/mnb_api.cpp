@@ -206,7 +206,6 @@ int32_t mnb_context_destroy(mnb_context *ctx) {
     if (ctx->stage_x) note(hipFree(ctx->stage_x));
     if (ctx->stage_y) note(hipFree(ctx->stage_y));
     if (ctx->sk_ws) note(hipFree(ctx->sk_ws));
-    if (ctx->sk_cnt) note(hipFree(ctx->sk_cnt));
     note(hipStreamDestroy(ctx->stream));
     delete ctx;
     if (first != hipSuccess) return hip_fail(first, "close");
@@ -537,14 +536,12 @@ int32_t mnb_supports_batch(const mnb_weight *w) { return w ? 1 : 0; }
 
 int32_t mnb_max_batch_rows(void) { return std::numeric_limits<int32_t>::max() / 2; }
 
-// M > 16: stream-K GEMM over one persistent workgroup per CU.  The partial
-// tile workspace (sized for one workgroup per CU) and the per-tile arrival
-// counters (at least 16384 tiles, e.g. M = 4096 x N = 1M) live in the context
-// and are allocated on first use, so later calls -- and graphs captured from
-// them -- keep the same buffers; new counters are zeroed once, and every
-// launch leaves them zero again.  The kernel addresses x and the weights with
-// 32-bit byte offsets: rows of x go in chunks of at most 2 GiB, and packed
-// weights of 4 GiB or more are refused.
+// M > 16: stream-K GEMM over one persistent workgroup per CU.  The workspace
+// for the partial tiles of split tiles (sized for one workgroup per CU) lives
+// in the context and is allocated on first use, so later calls -- and graphs
+// captured from them -- keep the same buffer.  The kernel addresses x and the
+// weights with 32-bit byte offsets: rows of x go in chunks of at most 2 GiB,
+// and packed weights of 4 GiB or more are refused.
 static hipError_t launch_prefill(mnb_context *ctx, const mnb_weight *w, const mnb::MatmulArgs &a, hipStream_t s) {
     const mnb::WeightGeom &g = w->g;
     if ((uint64_t)g.NT * (uint64_t)g.ST * mnb::kTileBytes >= ((uint64_t)1 << 32)) return hipErrorInvalidValue;
@@ -552,11 +549,6 @@ static hipError_t launch_prefill(mnb_context *ctx, const mnb_weight *w, const mn
     const int chunk = (int)std::min<int64_t>(a.M, chunk_rows);
     hipError_t e = ensure(&ctx->sk_ws, &ctx->sk_ws_cap, mnb::sk_workspace_bytes(ctx->cu_count));
     if (e != hipSuccess) return e;
-    const size_t cnt_bytes = (size_t)std::max(mnb::sk_tiles(chunk, g.NT), 16384) * sizeof(int32_t);
-    if (ctx->sk_cnt_cap < cnt_bytes || !ctx->sk_cnt) {
-        if ((e = ensure(&ctx->sk_cnt, &ctx->sk_cnt_cap, cnt_bytes)) != hipSuccess) return e;
-        if ((e = hipMemsetAsync(ctx->sk_cnt, 0, ctx->sk_cnt_cap, s)) != hipSuccess) return e;
-    }
     const size_t y_row = (size_t)g.N * (a.y_type == MNB_F16 ? 2 : 4);
     for (int m0 = 0; m0 < a.M; m0 += chunk) {
         mnb::MatmulArgs c = a;
@@ -564,7 +556,7 @@ static hipError_t launch_prefill(mnb_context *ctx, const mnb_weight *w, const mn
         c.x = a.x + (size_t)m0 * a.ldx;
         c.y = (unsigned char *)a.y + (size_t)m0 * y_row;
         const int G = mnb::sk_grid(mnb::sk_tiles(c.M, g.NT), g.ST, ctx->cu_count);
-        if ((e = mnb::launch_gemm_sk(w, c, G, (float *)ctx->sk_ws, (int32_t *)ctx->sk_cnt, s)) != hipSuccess) return e;
+        if ((e = mnb::launch_gemm_sk(w, c, G, (float *)ctx->sk_ws, s)) != hipSuccess) return e;
     }
     return hipSuccess;
 }

@@ -7,26 +7,32 @@
 //
 // Output tile 128 (M) x 256 (N) per workgroup of 8 waves (two per SIMD, so
 // one wave's LDS and dequant latency hides behind the other's MFMAs), each
-// wave 64 x 64 (4 x 4 fragments of v_mfma_f32_16x16x32_f16, fp32 accumulators).
+// wave 128 x 32: four 32-row x fragments against one 32-column weight
+// fragment of v_mfma_f32_32x32x16_f16, fp32 accumulators.  The weight
+// fragment is the MFMA's A operand and x its B operand, so the accumulators
+// hold y transposed: each lane owns four consecutive columns of one row per
+// 4-register group and writes them with one 8-byte (fp16) or 16-byte (fp32)
+// store.
 // Operand pipeline, one 128-k stage at a time: every operand of stage s + 2 --
 // the x tile (32 KiB), the packed weight tiles (16 KiB), their scales and zero
 // points -- is copied straight from HBM into a 3-slot LDS ring by direct
 // global->LDS loads while stage s computes, so no load ever passes through
-// registers and two stages of latency are hidden.  Per 32-k step a wave reads
-// its four raw weight fragments from the ring, dequantizes them in registers
-// (w = (q - zp) * scale, scale folded into the fp16 operand) and runs 16 MFMAs
-// against four x fragments (the two waves of an N quarter dequantize the same
-// tiles).  x rows are stored with chunk c of row m at slot c ^ (m & 15), so
-// the fragment reads are free of bank conflicts.
+// registers and two stages of latency are hidden.  Per 16-k step a wave
+// dequantizes its weight fragment in registers (w = (q - zp) * scale, scale
+// folded into the fp16 operand) and runs 4 MFMAs against four x fragments.
+// x rows are stored with chunk c of row m at slot c ^ (m & 15), so the
+// fragment reads are free of bank conflicts.
 //
 // Stream-K: the grid is one persistent workgroup per CU.  The (tile, stage)
 // iterations of the whole product are cut into equal contiguous ranges, one
 // per workgroup, so every CU gets the same MFMA work whatever the tile count.
-// A tile whose stages span several workgroups is finished by whichever
-// contributor arrives last (fp32 partials in a workspace, a per-tile arrival
-// counter that the finisher resets); no workgroup ever waits for another.
-// Logical workgroup ids are laid out XCD-contiguous, so neighbouring
-// workgroups (which share tiles and weight columns) sit on the same XCD.
+// A workgroup that owns all stages of a tile writes y directly.  A tile whose
+// stages span several workgroups is written as fp32 partial tiles, one per
+// contributor, and summed in contributor order by sk_reduce_kernel, launched
+// right after on the same stream over the whole chip; no workgroup ever
+// waits for another.  Logical workgroup ids are laid out XCD-contiguous, so
+// neighbouring workgroups (which share tiles and weight columns) sit on the
+// same XCD.
 #include <algorithm>
 
 #include "mnb_device.h"
@@ -40,7 +46,9 @@ constexpr int kSkBN = kSkWaves * kSkNTW * kTileRows;   // 256 columns per tile
 constexpr int kSkFM = kSkBM / 32;   // 32-row A fragments per wave
 constexpr int kSkFN = kSkNTW / 2;   // 32-column B fragments per wave
 constexpr int kSkThreads = 64 * kSkWaves;
-constexpr int kSkPartialFloats = kSkThreads * kSkFM * kSkFN * 16;   // one partial tile
+constexpr int kSkPartialFloats = kSkBM * kSkBN;   // one fp32 partial tile, [kSkBM][kSkBN] row-major
+constexpr int kSkReduceRows = 16;                 // rows of a partial tile per reduce workgroup
+constexpr int kSkReduceThreads = 256;             // each thread: 4 rows x 4 columns
 
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
@@ -56,10 +64,10 @@ struct SkParams {
     int32_t ldx, kx, M, N, NT, ST;
     void *y;
     int32_t y_f16, accumulate;
+    int32_t y_vec;          // N % 4 == 0 and y aligned for 4-element stores
     int32_t MT, T, G;       // m-tiles, tiles, workgroups
     int32_t I;              // iterations = T * ST (below 2^31)
-    float *ws;              // [G][2] partial tiles
-    int32_t *cnt;           // [T] arrival counters (zero between launches)
+    float *ws;              // [G][2] partial tiles: slot 0 for a workgroup's first tile, 1 for its last
 };
 
 // first iteration of logical workgroup g (g = G gives I)
@@ -71,6 +79,45 @@ __device__ __forceinline__ int sk_owner(int i, const SkParams &p) {
     while (g + 1 < p.G && sk_start(g + 1, p) <= i) ++g;
     while (g > 0 && sk_start(g, p) > i) --g;
     return g;
+}
+
+// Four consecutive outputs y[m, n..n+3] (=|+=) v, m < M checked by the
+// caller; columns >= N are dropped.  One 8-byte (fp16) or 16-byte (fp32)
+// store when the row segment is whole and aligned.
+__device__ __forceinline__ void store_y4(const SkParams &p, int m, int n, float4_t v) {
+    const size_t idx = (size_t)m * p.N + n;
+    const bool acc = p.accumulate != 0;
+    if (p.y_vec && n + 3 < p.N) {
+        if (p.y_f16) {
+            __attribute__((address_space(1))) u32x2_t *q = (__attribute__((address_space(1))) u32x2_t *)((_Float16 *)p.y + idx);
+            if (acc) {
+                const u32x2_t o = *q;
+                const half2_t o0 = as_half2(o[0]), o1 = as_half2(o[1]);
+                v[0] += (float)o0[0];
+                v[1] += (float)o0[1];
+                v[2] += (float)o1[0];
+                v[3] += (float)o1[1];
+            }
+            half2_t h0, h1;
+            h0[0] = (_Float16)v[0];
+            h0[1] = (_Float16)v[1];
+            h1[0] = (_Float16)v[2];
+            h1[1] = (_Float16)v[3];
+            *q = (u32x2_t){as_u32(h0), as_u32(h1)};
+        } else {
+            __attribute__((address_space(1))) float4_t *q = (__attribute__((address_space(1))) float4_t *)((float *)p.y + idx);
+            if (acc) v += *q;
+            *q = v;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (n + e < p.N) {
+                if (p.y_f16) store_y<true>(p.y, idx + e, v[e], acc);
+                else store_y<false>(p.y, idx + e, v[e], acc);
+            }
+        }
+    }
 }
 
 // LDS byte address of a pointer into a __shared__ array.
@@ -113,7 +160,6 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     constexpr int ZB = L::ZB;
     constexpr int D = L::kDepth;
     __shared__ __align__(1024) unsigned char ring[D][L::kBytes];
-    __shared__ int s_last;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -233,83 +279,41 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             for (int v = 0; v < 16; ++v) acc[a][f][v] = 0.f;
 
     // ---- epilogue of tile t after nst of its stages ----
+    // Fragment (a, f), register v of lane (c32, h): row a * 32 + c32 of the
+    // tile, column 32 f + 8 (v / 4) + 4 h + v % 4 of the wave's 32 columns.
     int t = i0 / p.ST;
     auto epilogue = [&](int nst) __attribute__((always_inline)) {
         const int m0 = (t % p.MT) * kSkBM, ng = t / p.MT;
-        const int n_wave = (ng * L::kNT + wave * kSkNTW) * kTileRows;
-        bool write_out = nst == p.ST;
-        if (!write_out) {
-            // Partial tiles travel through agent-scope relaxed atomics (stores
-            // and loads that are coherent across XCDs without writing back or
-            // invalidating any L2): each thread waits for its own stores to
-            // complete before the workgroup bumps the tile's arrival counter,
-            // and the finisher reads only after the counter told it so.
-            typedef unsigned long long u64;
+        const int c_wave = wave * kSkNTW * kTileRows;   // first column of this wave in the tile
+        if (nst == p.ST) {
+            const int n_wave = ng * kSkBN + c_wave;
+#pragma unroll
+            for (int a = 0; a < kSkFM; ++a) {
+                const int m = m0 + a * 32 + c32;
+                if (m < p.M) {
+#pragma unroll
+                    for (int f = 0; f < kSkFN; ++f)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            store_y4(p, m, n_wave + f * 32 + 8 * j + 4 * h,
+                                     (float4_t){acc[a][f][4 * j], acc[a][f][4 * j + 1], acc[a][f][4 * j + 2],
+                                                acc[a][f][4 * j + 3]});
+                }
+            }
+        } else {
+            // partial tile of a split tile: [kSkBM][kSkBN] fp32, summed by sk_reduce_kernel
             const int slot = i0 / p.ST == t ? 0 : 1;   // 0 if t is this workgroup's first tile
-            u64 *mine = (u64 *)(p.ws + ((size_t)g * 2 + slot) * kSkPartialFloats) + tid;
+            __attribute__((address_space(1))) float *part =
+                (__attribute__((address_space(1))) float *)p.ws + ((size_t)g * 2 + slot) * kSkPartialFloats;
 #pragma unroll
             for (int a = 0; a < kSkFM; ++a)
 #pragma unroll
                 for (int f = 0; f < kSkFN; ++f)
 #pragma unroll
-                    for (int v2 = 0; v2 < 8; ++v2) {
-                        const u64 bits = (u64)__float_as_uint(acc[a][f][2 * v2]) |
-                                         ((u64)__float_as_uint(acc[a][f][2 * v2 + 1]) << 32);
-                        __hip_atomic_store(mine + ((a * kSkFN + f) * 8 + v2) * kSkThreads, bits, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                    }
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
-            const int g_first = sk_owner(t * p.ST, p);
-            const int g_last = sk_owner((t + 1) * p.ST - 1, p);
-            if (tid == 0)
-                s_last = __hip_atomic_fetch_add(&p.cnt[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                         g_last - g_first;
-            __syncthreads();
-            if (s_last) {
-                // every contributor's partial (this workgroup's included) is read
-                // back and summed in contributor order, whoever finishes: the
-                // result does not depend on arrival order
-                for (int og = g_first; og <= g_last; ++og) {
-                    const int oslot = sk_start(og, p) / p.ST == t ? 0 : 1;
-                    const u64 *part = (const u64 *)(p.ws + ((size_t)og * 2 + oslot) * kSkPartialFloats) + tid;
-#pragma unroll
-                    for (int a = 0; a < kSkFM; ++a)
-#pragma unroll
-                        for (int f = 0; f < kSkFN; ++f)
-#pragma unroll
-                            for (int v2 = 0; v2 < 8; ++v2) {
-                                const u64 bits = __hip_atomic_load(part + ((a * kSkFN + f) * 8 + v2) * kSkThreads,
-                                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                                const float lo = __uint_as_float((uint32_t)bits), hi = __uint_as_float((uint32_t)(bits >> 32));
-                                acc[a][f][2 * v2] = og == g_first ? lo : acc[a][f][2 * v2] + lo;
-                                acc[a][f][2 * v2 + 1] = og == g_first ? hi : acc[a][f][2 * v2 + 1] + hi;
-                            }
-                }
-                if (tid == 0) __hip_atomic_store(&p.cnt[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // ready for the next launch
-                write_out = true;
-            }
-        }
-        if (write_out) {
-            // fragment (a, f): lane holds column c32, rows 8 (v / 4) + 4 h + v % 4
-            const bool accum = p.accumulate != 0;
-#pragma unroll
-            for (int f = 0; f < kSkFN; ++f) {
-                const int n = n_wave + f * 32 + c32;
-                if (n >= p.N) continue;
-#pragma unroll
-                for (int a = 0; a < kSkFM; ++a) {
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        const int mm = m0 + a * 32 + 8 * (v / 4) + 4 * h + (v % 4);
-                        if (mm < p.M) {
-                            const size_t idx = (size_t)mm * p.N + n;
-                            if (p.y_f16) store_y<true>(p.y, idx, acc[a][f][v], accum);
-                            else store_y<false>(p.y, idx, acc[a][f][v], accum);
-                        }
-                    }
-                }
-            }
+                    for (int j = 0; j < 4; ++j)
+                        *(__attribute__((address_space(1))) float4_t *)(part + (a * 32 + c32) * kSkBN + c_wave + f * 32 +
+                                                                         8 * j + 4 * h) =
+                            (float4_t){acc[a][f][4 * j], acc[a][f][4 * j + 1], acc[a][f][4 * j + 2], acc[a][f][4 * j + 3]};
         }
 #pragma unroll
         for (int a = 0; a < kSkFM; ++a)
@@ -397,7 +401,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
 #pragma unroll
                 for (int a = 0; a < kSkFM; ++a)
 #pragma unroll
-                    for (int f = 0; f < kSkFN; ++f) acc[a][f] = mfma32x32x16(af[s & 1][a], bf[s & 1][f], acc[a][f]);
+                    for (int f = 0; f < kSkFN; ++f) acc[a][f] = mfma32x32x16(bf[s & 1][f], af[s & 1][a], acc[a][f]);
                 // order within the step: the next step's x reads go out first,
                 // between the MFMAs, and its dequant VALU fills the MFMA shadow
                 if (s + 1 < kTileK / 16) {
@@ -429,38 +433,113 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// Sums the partial tiles of every split tile in contributor order and writes
+// y.  Workgroup (b, rb) looks at the boundary between logical workgroups b
+// and b + 1 (b < G - 1); when that boundary falls inside tile t and is the
+// first boundary inside t, it reduces rows [rb * kSkReduceRows, +kSkReduceRows)
+// of t.  The contributors' partial-tile offsets are computed once per
+// workgroup into LDS; each thread owns four rows of one 4-column group and
+// keeps the loads of two contributors (eight 16-byte loads) in flight.
+__global__ __launch_bounds__(kSkReduceThreads) void sk_reduce_kernel(SkParams p) {
+    constexpr int kRowBlocks = kSkBM / kSkReduceRows;
+    constexpr int kColGroups = kSkBN / 4;
+    constexpr int kRowsPerThread = kSkReduceRows * kColGroups / kSkReduceThreads;
+    __shared__ uint32_t s_part[kSkReduceThreads];   // partial-tile index (2 og + slot) of contributor i
+    const int b = (int)blockIdx.x / kRowBlocks + 1;   // boundary at sk_start(b)
+    const int rb = (int)blockIdx.x % kRowBlocks;
+    const int s = sk_start(b, p);
+    if (s % p.ST == 0) return;                        // between tiles: no split
+    const int t = s / p.ST;
+    if (sk_start(b - 1, p) > t * p.ST) return;        // an earlier boundary of t does the work
+    const int g_first = b - 1, g_last = sk_owner((t + 1) * p.ST - 1, p);
+    const int nc = g_last - g_first + 1;              // contributors, at most G <= kSkReduceThreads
+    const int tid = (int)threadIdx.x;
+    if (tid < nc) {
+        const int og = g_first + tid;
+        s_part[tid] = (uint32_t)(og * 2 + (sk_start(og, p) / p.ST == t ? 0 : 1));
+    }
+    __syncthreads();
+    const int c = (tid % kColGroups) * 4;
+    const int r0 = rb * kSkReduceRows + tid / kColGroups;
+    const int m0 = (t % p.MT) * kSkBM, n = (t / p.MT) * kSkBN + c;
+    if (n >= p.N) return;
+    float4_t sum[kRowsPerThread];
+    auto part = [&](int i, int k) __attribute__((always_inline)) {
+        return gld((const float4_t *)(p.ws + (size_t)s_part[i] * kSkPartialFloats +
+                                       (r0 + k * (kSkReduceThreads / kColGroups)) * kSkBN + c));
+    };
+    int i = 0;
+    for (; i + 1 < nc; i += 2) {
+        float4_t a[kRowsPerThread], bb[kRowsPerThread];
+#pragma unroll
+        for (int k = 0; k < kRowsPerThread; ++k) {
+            a[k] = part(i, k);
+            bb[k] = part(i + 1, k);
+        }
+#pragma unroll
+        for (int k = 0; k < kRowsPerThread; ++k) sum[k] = (i == 0 ? a[k] : sum[k] + a[k]) + bb[k];
+    }
+    if (i < nc) {
+#pragma unroll
+        for (int k = 0; k < kRowsPerThread; ++k) sum[k] = sum[k] + part(i, k);   // nc >= 2, so i > 0 here
+    }
+#pragma unroll
+    for (int k = 0; k < kRowsPerThread; ++k) {
+        const int m = m0 + r0 + k * (kSkReduceThreads / kColGroups);
+        if (m < p.M) store_y4(p, m, n, sum[k]);
+    }
+}
+
 size_t sk_workspace_bytes(int G) { return (size_t)G * 2 * kSkPartialFloats * sizeof(float); }
 
 int sk_tiles(int M, int NT) { return ((M + kSkBM - 1) / kSkBM) * ((NT * kTileRows + kSkBN - 1) / kSkBN); }
 
-// Candidates: G = m T (m = 1, 2, ...: every tile split into about m pieces)
-// and G = cu_count.  Estimated time, fitted to measurements on MI355X over
-// the Phi-3 projection shapes at M = 128..2048: a stage costs 1.5 us on a
-// lightly loaded chip up to 2.4 us with every CU busy; a split tile costs a
-// fixed 8 us plus 3 us per contributing workgroup (partial tiles written and
-// read back through the coherent path).
+// Estimated time of G workgroups (us).  A least-squares fit (4% median error)
+// to 300 timings on MI355X of the Phi-3 projections at M = 128, 512 and 2048
+// over every candidate G: a stage costs 1.16 us plus 0.38 us times the busy
+// fraction of the chip, each tile a workgroup touches 8.6 us (pipeline fill
+// and epilogue), and split tiles 0.28 us per MB of partial tiles (stored, then
+// read by the reduce kernel) less 2 us, plus 1.7 us when every CU holds a
+// split workgroup.
+static double sk_cost(int64_t T, int64_t ST, int64_t G, int cu_count) {
+    const int64_t I = T * ST;
+    const int64_t per_wg = (I + G - 1) / G;
+    bool split = false;
+    for (int64_t b = 1; b < G && !split; ++b) split = (b * I / G) % ST != 0;
+    const double load = (double)std::min<int64_t>(G, cu_count) / cu_count;
+    const double tiles = (double)((per_wg + ST - 1) / ST + (split ? 1 : 0));
+    double t = (double)per_wg * (1.16 + 0.38 * load) + 8.6 * tiles;
+    if (split) {
+        const double partial_mb = (double)(G + std::min<int64_t>(G, T)) * kSkPartialFloats * 4.0 / 1.0e6;
+        t += 0.28 * partial_mb - 2.0 + (G > cu_count - 8 ? 1.7 : 0.0);
+    }
+    return t;
+}
+
+// Candidates: every workgroup count that gives each workgroup whole tiles (G
+// dividing T), every tile cut into m equal pieces (G = m T), one workgroup per
+// CU, and two CUs per XCD fewer; the cheapest by sk_cost wins.  G never
+// exceeds the CU count (one persistent workgroup per CU) nor kSkReduceThreads
+// (one reduce thread per contributor).
 int sk_grid(int T, int ST, int cu_count) {
     const int64_t I = (int64_t)T * ST;
-    auto cost = [&](int64_t G) {
-        const double per_wg = (double)((I + G - 1) / G);
-        const double t_stage = 1.5 + 0.9 * (double)std::min<int64_t>(G, cu_count) / cu_count;
-        double t = per_wg * t_stage;
-        if (G > T) t += 8.0 + 3.0 * (double)((ST + (int64_t)per_wg - 1) / (int64_t)per_wg + 1);
-        return t;
+    const int64_t cap = std::min<int64_t>(std::min<int64_t>(cu_count, kSkReduceThreads), I);
+    int64_t best = 0;
+    double best_t = 0.0;
+    auto consider = [&](int64_t G) {
+        if (G < 1 || G > cap) return;
+        const double t = sk_cost(T, ST, G, cu_count);
+        if (best == 0 || t < best_t) best = G, best_t = t;
     };
-    const int64_t cap = std::min<int64_t>(cu_count, I);
-    int64_t best = std::min<int64_t>(T, cap);
-    double best_t = cost(best);
-    for (int64_t G = 2 * (int64_t)T; G < cap; G += T) {
-        const double t = cost(G);
-        if (t < best_t) best = G, best_t = t;
-    }
-    if (cost(cap) < best_t) best = cap;
+    for (int64_t k = 1; k <= T; ++k)
+        if (T % k == 0) consider(T / k);
+    for (int64_t G = 2 * (int64_t)T; G <= cap; G += T) consider(G);
+    consider(cap);
+    consider(cap - 16);
     return (int)best;
 }
 
-hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, int32_t *cnt,
-                          hipStream_t stream) {
+hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, hipStream_t stream) {
     const WeightGeom &g = w->g;
     SkParams p;
     p.q_t = (const u32x4_t *)w->q_t;
@@ -476,6 +555,7 @@ hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float
     p.y = a.y;
     p.y_f16 = a.y_type == MNB_F16;
     p.accumulate = a.accumulate;
+    p.y_vec = (g.N % 4 == 0) && ((uintptr_t)a.y % (p.y_f16 ? 8 : 16) == 0);
     p.MT = (a.M + kSkBM - 1) / kSkBM;
     p.T = sk_tiles(a.M, g.NT);
     p.G = G;
@@ -483,7 +563,6 @@ hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float
     if (iters >= (int64_t)1 << 31) return hipErrorInvalidValue;
     p.I = (int32_t)iters;
     p.ws = ws;
-    p.cnt = cnt;
     dim3 grid(G), block(kSkThreads);
 #define MNB_SK_LAUNCH(ST_, ZP_, SPS_) hipLaunchKernelGGL((gemm_sk_kernel<ST_, ZP_, SPS_>), grid, block, 0, stream, p)
 #define MNB_SK_SPS(ST_, ZP_)                           \
@@ -501,7 +580,16 @@ hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float
     }
 #undef MNB_SK_SPS
 #undef MNB_SK_LAUNCH
-    return hipGetLastError();
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // split tiles exist when some range boundary falls inside a tile
+    bool split = false;
+    for (int b = 1; b < G && !split; ++b) split = ((int64_t)b * p.I / G) % g.ST != 0;
+    if (split) {
+        hipLaunchKernelGGL(sk_reduce_kernel, dim3((G - 1) * (kSkBM / kSkReduceRows)), dim3(kSkReduceThreads), 0, stream, p);
+        e = hipGetLastError();
+    }
+    return e;
 }
 
 }  // namespace mnb

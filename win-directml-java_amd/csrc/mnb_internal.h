@@ -65,11 +65,9 @@ struct mnb_context {
     size_t stage_x_cap = 0;
     void *stage_y = nullptr;
     size_t stage_y_cap = 0;
-    // stream-K GEMM: partial tiles and per-tile arrival counters
+    // stream-K GEMM: fp32 partial tiles of split tiles
     void *sk_ws = nullptr;
     size_t sk_ws_cap = 0;
-    void *sk_cnt = nullptr;
-    size_t sk_cnt_cap = 0;
     mnb_device_info info{};
 };
 
@@ -167,16 +165,15 @@ int stream_kernel_waves_per_cu(int scale_f32, int has_zp, int sps);
 constexpr int kStreamWavesPerBlock = 4;
 
 // Stream-K GEMM (M > 16): G persistent workgroups share the (tile, k-stage)
-// iterations; ws holds sk_workspace_bytes(G) of fp32 partial tiles, cnt one
-// arrival counter per tile (sk_tiles), zero before the first launch (the
-// kernel leaves them zero).
+// iterations; ws holds sk_workspace_bytes(G) of fp32 partial tiles for the
+// tiles whose stages span workgroups, which a second kernel on the same
+// stream sums in contributor order.
 size_t sk_workspace_bytes(int G);
 int sk_tiles(int M, int NT);
 // Workgroup count for T tiles of ST stages on cu_count CUs (a cost model:
 // whole tiles per workgroup when that is cheapest, else stream-K).
 int sk_grid(int T, int ST, int cu_count);
-hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, int32_t *cnt,
-                          hipStream_t stream);
+hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, hipStream_t stream);
 
 // largest M handled by the skinny (GEMV-style) kernel
 constexpr int kSkinnyMaxM = 16;
