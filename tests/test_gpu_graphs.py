@@ -1,0 +1,93 @@
+"""Resident activations and graph capture (the record-into semantics of
+MatMulNBitsKernel.recordResidentInto / recordIntoGpuResident,
+directml-windows-bindings/.../windows/MatMulNBitsKernel.java:1687-1832,
+and the batched recording of WarpExecutionContext.java:131-160).
+
+Products on device pointers allocate nothing and record only kernel launches,
+so a sequence of them -- single-row products, a prefill product whose tiles
+are split over workgroups (GEMM plus its reduce kernel), and a group launch --
+is captured into a HIP graph on a fresh context, with no eager call first.
+Each replay, with new activations written by eager work between replays,
+equals the eager calls bit for bit."""
+import numpy as np
+import pytest
+
+import mnb_hip
+from mnb_hip import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _weight(ctx, seed, N, K, bs=32, zp=False):
+    t = synth.make_weight(seed, N, K, bs, with_zp=zp)
+    if zp:
+        return mnb_hip.Weight(ctx, N, K, bs, t.q, t.scales_f16, t.zp_row_padded, mnb_hip.MNB_ZP_ROW_PADDED)
+    return mnb_hip.Weight(ctx, N, K, bs, t.q, t.scales_f16)
+
+
+def test_graph_capture_replays_match_eager():
+    import torch
+    ctx = mnb_hip.Context(0)
+    try:
+        dev = "cuda"
+        w_o = _weight(ctx, 1, 3072, 3072)                  # decode o_proj
+        w_gu = _weight(ctx, 2, 16384, 3072)                # decode gate_up
+        w_pf = _weight(ctx, 3, 1000, 3072, zp=True)        # prefill product with split tiles
+        w_g = [_weight(ctx, 10 + i, 1536, 576, 64, zp=True) for i in range(3)]
+        gen = torch.Generator(device=dev).manual_seed(7)
+        x1 = torch.empty(3072, device=dev, dtype=torch.float16)
+        xp = torch.empty(200, 3072, device=dev, dtype=torch.float16)
+        xg = [torch.empty(576, device=dev, dtype=torch.float16) for _ in w_g]
+        y_o = torch.empty(3072, device=dev, dtype=torch.float16)
+        y_gu = torch.empty(16384, device=dev, dtype=torch.float32)
+        y_pf = torch.empty(200, 1000, device=dev, dtype=torch.float16)
+        y_g = [torch.empty(1536, device=dev, dtype=torch.float16) for _ in w_g]
+        st = torch.cuda.Stream()
+
+        def fill():
+            x1.copy_(torch.randn(3072, device=dev, generator=gen).half())
+            xp.copy_(torch.randn(200, 3072, device=dev, generator=gen).half())
+            for x in xg:
+                x.copy_(torch.randn(576, device=dev, generator=gen).half())
+
+        with torch.cuda.stream(st):
+            fill()
+        torch.cuda.synchronize()
+        group = mnb_hip.Group(ctx, list(zip(w_g, xg, y_g)))
+
+        def record():
+            w_o.matmul(x1, y_o, stream=st.cuda_stream)
+            w_gu.matmul(x1, y_gu, stream=st.cuda_stream)
+            w_pf.matmul(xp, y_pf, stream=st.cuda_stream)
+            group.run(st.cuda_stream)
+
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=st):
+            record()
+        torch.cuda.synchronize()
+
+        outs = [y_o, y_gu, y_pf] + y_g
+        for rep in range(4):
+            with torch.cuda.stream(st):
+                fill()
+                for y in outs:
+                    y.fill_(float("nan"))
+                graph.replay()
+            torch.cuda.synchronize()
+            got = [y.clone() for y in outs]
+            with torch.cuda.stream(st):
+                for y in outs:
+                    y.fill_(float("nan"))
+                record()
+            torch.cuda.synchronize()
+            for i, (a, b) in enumerate(zip(got, outs)):
+                assert torch.isfinite(a).all(), (rep, i)
+                assert torch.equal(a.view(torch.int16) if a.dtype == torch.float16 else a.view(torch.int32),
+                                   b.view(torch.int16) if b.dtype == torch.float16 else b.view(torch.int32)), (rep, i)
+        group.close()
+        for w in [w_o, w_gu, w_pf] + w_g:
+            w.close()
+        del graph
+    finally:
+        torch.cuda.synchronize()
+        ctx.close()

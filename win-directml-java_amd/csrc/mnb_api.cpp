@@ -177,6 +177,15 @@ int32_t mnb_context_create(int32_t device, mnb_context **out) {
         delete c;
         return hip_fail(e, "init");
     }
+    // the stream-K GEMM's partial-tile workspace (one workgroup per CU) is
+    // allocated here, so products on device pointers allocate nothing and can
+    // be captured into a HIP graph from the first call
+    e = ensure(&c->sk_ws, &c->sk_ws_cap, mnb::sk_workspace_bytes(c->cu_count));
+    if (e != hipSuccess) {
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return hip_fail(e, "init");
+    }
     mnb_device_info &i = c->info;
     snprintf(i.name, sizeof i.name, "%s", prop.name);
     snprintf(i.arch, sizeof i.arch, "%s", prop.gcnArchName);
@@ -538,8 +547,8 @@ int32_t mnb_max_batch_rows(void) { return std::numeric_limits<int32_t>::max() / 
 
 // M > 16: stream-K GEMM over one persistent workgroup per CU.  The workspace
 // for the partial tiles of split tiles (sized for one workgroup per CU) lives
-// in the context and is allocated on first use, so later calls -- and graphs
-// captured from them -- keep the same buffer.  The kernel addresses x and the
+// in the context and is allocated with it, so every call -- and graphs
+// captured from them -- uses the same buffer.  The kernel addresses x and the
 // weights with 32-bit byte offsets: rows of x go in chunks of at most 2 GiB,
 // and packed weights of 4 GiB or more are refused.
 static hipError_t launch_prefill(mnb_context *ctx, const mnb_weight *w, const mnb::MatmulArgs &a, hipStream_t s) {

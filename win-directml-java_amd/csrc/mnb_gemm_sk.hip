@@ -140,18 +140,22 @@ struct SkSlot {
     static constexpr int kNT = kSkBN / kTileRows;                   // 16 n-tiles per tile
     static constexpr int kX = 0;                                    // x tile [128][16 chunks]
     static constexpr int kQ = kSkBM * kTileK * 2;                   // 32 KiB: packed tiles [16][64 lanes][16 B]
+    static constexpr int kWin = 1024;                               // bytes of one 64-lane direct load
     static constexpr int kS = kQ + kNT * kTileBytes;                // scales [16 tiles][16 rows][SPS]
     static constexpr int kTileS = kTileRows * SPS * (int)sizeof(ScaleT);   // scale bytes per tile
-    static constexpr int kZ = kS + kNT * kTileS;                    // zero points [16 tiles][16 rows][ZB]
+    static constexpr int kSRegion = kNT * kTileS > kWin ? kNT * kTileS : kWin;   // padded to one window
+    static constexpr int kZ = kS + kSRegion;                        // zero points [16 tiles][16 rows][ZB]
     static constexpr int kTileZ = kTileRows * ZB;
-    static constexpr int kBytes = kZ + (HAS_ZP ? kNT * kTileZ : 0);
+    static constexpr int kZRegion = HAS_ZP ? (kNT * kTileZ > kWin ? kNT * kTileZ : kWin) : 0;
+    static constexpr int kBytes = kZ + kZRegion;
     static constexpr int kDepth = 3 * kBytes <= 160 * 1024 ? 3 : 2;   // ring slots (fits the 160 KiB LDS)
-    // per wave and stage: x pieces of 4 rows, its 4 packed tiles, their
-    // scales and zero points
-    static constexpr int kXDma = kSkBM * kTileK * 2 / 1024 / kSkWaves;
-    static constexpr int kSDma = (kSkNTW * kTileS + 1023) / 1024;
-    static constexpr int kDma = kXDma + kSkNTW + kSDma + (HAS_ZP ? 1 : 0);
-    static_assert(kTileS % 16 == 0 && kTileZ % 16 == 0 && kSkNTW * kTileZ <= 1024, "16-byte pieces");
+    // per wave and stage: x pieces of 4 rows, its packed tiles, and one
+    // 1 KiB window each of the scale and zero-point regions that contains
+    // the wave's own tiles (all 64 lanes load: no lane mask, no branch)
+    static constexpr int kXDma = kSkBM * kTileK * 2 / kWin / kSkWaves;
+    static constexpr int kDma = kXDma + kSkNTW + 1 + (HAS_ZP ? 1 : 0);
+    static_assert(kTileS % 16 == 0 && kTileZ % 16 == 0, "16-byte pieces");
+    static_assert(kSkNTW * kTileS <= kWin && kSkNTW * kTileZ <= kWin, "a wave's scales fit one window");
 };
 
 template <typename ScaleT, bool HAS_ZP, int SPS>
@@ -178,64 +182,58 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     // The issue cursor (tile lt, stage lst) stops at this workgroup's last
     // iteration, so every stage issues the same loads (the final ones re-load
     // the last stage into a slot nobody reads).  Lane byte offsets are set
-    // per tile; a stage only moves the scalar bases.
-    constexpr int SL = L::kTileS / 16;   // 16-byte scale pieces per tile
-    constexpr int ZL = L::kTileZ / 16;   // 16-byte zero-point pieces per tile
+    // per tile; a stage only moves the scalar bases.  issue_dma is straight
+    // -line code (no branch, no lane mask), so it can be interleaved with
+    // MFMAs; advance moves the cursor.
+    // Scales and zero points: the wave loads the 1 KiB window of the region
+    // that starts at its own tiles, moved back to end at the region's end;
+    // waves write identical bytes where windows overlap, and lanes past the
+    // workgroup's 16 n-tiles fill the padding.
+    constexpr int s_win_max = L::kSRegion - L::kWin;
+    constexpr int z_win_max = L::kZRegion - L::kWin;
+    const int s_win = min(wave * kSkNTW * L::kTileS, s_win_max);
+    const int z_win = HAS_ZP ? min(wave * kSkNTW * L::kTileZ, z_win_max) : 0;
     int lt = i0 / p.ST, lst = i0 - lt * p.ST, li = i0, lslot = 0;
-    uint32_t xrow[L::kXDma], xcol[L::kXDma], qoff[kSkNTW], soff[L::kSDma], zoff = 0;
+    uint32_t xrow[L::kXDma], xcolk[L::kXDma], qoff[kSkNTW], soff = 0, zoff = 0;
     auto set_tile = [&]() __attribute__((always_inline)) {
-        const int m0 = (lt % p.MT) * kSkBM, nt0 = (lt / p.MT) * L::kNT + wave * kSkNTW;
+        const int m0 = (lt % p.MT) * kSkBM, ntg = (lt / p.MT) * L::kNT, nt0 = ntg + wave * kSkNTW;
 #pragma unroll
         for (int u = 0; u < L::kXDma; ++u) {
             const int row = (wave * L::kXDma + u) * 4 + (lane >> 4);
             xrow[u] = (uint32_t)min(m0 + row, p.M - 1) * (uint32_t)p.ldx * 2u;
-            xcol[u] = (uint32_t)(((lane & 15) ^ (row & 15)) * 16);
+            xcolk[u] = (uint32_t)(((lane & 15) ^ (row & 15)) * 8);   // k of the chunk this lane loads
         }
 #pragma unroll
         for (int b = 0; b < kSkNTW; ++b)
             qoff[b] = ((uint32_t)min(nt0 + b, p.NT - 1) * (uint32_t)p.ST * 64u + (uint32_t)lane) * 16u;
-#pragma unroll
-        for (int v = 0; v < L::kSDma; ++v) {
-            const int l = min(v * 64 + lane, kSkNTW * SL - 1);
-            soff[v] = (uint32_t)min(nt0 + l / SL, p.NT - 1) * (uint32_t)p.ST * L::kTileS + (uint32_t)(l % SL) * 16u;
+        {
+            const int byte = s_win + lane * 16;
+            soff = (uint32_t)min(ntg + byte / L::kTileS, p.NT - 1) * (uint32_t)p.ST * L::kTileS +
+                   (uint32_t)(byte % L::kTileS);
         }
         if constexpr (HAS_ZP) {
-            const int l = min(lane, kSkNTW * ZL - 1);
-            zoff = (uint32_t)min(nt0 + l / ZL, p.NT - 1) * (uint32_t)p.ST * L::kTileZ + (uint32_t)(l % ZL) * 16u;
+            const int byte = z_win + lane * 16;
+            zoff = (uint32_t)min(ntg + byte / L::kTileZ, p.NT - 1) * (uint32_t)p.ST * L::kTileZ +
+                   (uint32_t)(byte % L::kTileZ);
         }
     };
     set_tile();
-    auto issue = [&]() __attribute__((always_inline)) {
-        const uint32_t base = ring0 + (uint32_t)(lslot * L::kBytes);
-        // x: this wave's kXDma pieces of 4 rows each; lane -> (row, slot)
-        if ((lst + 1) * kTileK <= p.kx) {
-            const unsigned char *xb = (const unsigned char *)p.x + (size_t)lst * kTileK * 2;
-#pragma unroll
-            for (int u = 0; u < L::kXDma; ++u)
-                dma16(base + L::kX + (uint32_t)(wave * L::kXDma + u) * 1024u, xrow[u] + xcol[u], xb);
-        } else {
-            // last stage with a k tail: chunks at k >= kx re-read the row's
-            // last chunk (zeroed in LDS on landing) and stay inside x
-#pragma unroll
-            for (int u = 0; u < L::kXDma; ++u) {
-                const uint32_t k = (uint32_t)min(lst * kTileK + (int)(xcol[u] / 2), p.kx - 8);
-                dma16(base + L::kX + (uint32_t)(wave * L::kXDma + u) * 1024u, xrow[u] + k * 2u, p.x);
-            }
-        }
-        // this wave's packed tiles, scales and zero points
-        const int ntl = wave * kSkNTW;   // first local n-tile
+    // x piece u of this wave (4 rows); chunks at k >= kx (a k tail) re-read
+    // the row's last chunk, stay inside x, and are zeroed in LDS on landing
+    auto dma_x = [&](uint32_t base, int u) __attribute__((always_inline)) {
+        const uint32_t k = (uint32_t)min(lst * kTileK + (int)xcolk[u], p.kx - 8);
+        dma16(base + L::kX + (uint32_t)(wave * L::kXDma + u) * 1024u, xrow[u] + k * 2u, p.x);
+    };
+    auto dma_q = [&](uint32_t base, int b) __attribute__((always_inline)) {
         const unsigned char *qb = (const unsigned char *)p.q_t + (size_t)lst * kTileBytes;
-#pragma unroll
-        for (int b = 0; b < kSkNTW; ++b) dma16(base + L::kQ + (uint32_t)(ntl + b) * kTileBytes, qoff[b], qb);
-        const unsigned char *sb = (const unsigned char *)p.s_t + (size_t)lst * L::kTileS;
-#pragma unroll
-        for (int v = 0; v < L::kSDma; ++v) {
-            if (v * 64 + lane < kSkNTW * SL) dma16(base + L::kS + (uint32_t)(ntl * L::kTileS + v * 1024), soff[v], sb);
-        }
-        if constexpr (HAS_ZP) {
-            const unsigned char *zb = p.zp_t + (size_t)lst * L::kTileZ;
-            if (lane < kSkNTW * ZL) dma16(base + L::kZ + (uint32_t)(ntl * L::kTileZ), zoff, zb);
-        }
+        dma16(base + L::kQ + (uint32_t)(wave * kSkNTW + b) * kTileBytes, qoff[b], qb);
+    };
+    auto dma_sz = [&](uint32_t base) __attribute__((always_inline)) {
+        dma16(base + L::kS + (uint32_t)s_win, soff, (const unsigned char *)p.s_t + (size_t)lst * L::kTileS);
+        if constexpr (HAS_ZP) dma16(base + L::kZ + (uint32_t)z_win, zoff, p.zp_t + (size_t)lst * L::kTileZ);
+    };
+    auto slot_base = [&]() __attribute__((always_inline)) { return ring0 + (uint32_t)(lslot * L::kBytes); };
+    auto advance = [&]() __attribute__((always_inline)) {
         if (li + 1 < i1) {
             ++li;
             if (++lst == p.ST) {
@@ -245,6 +243,15 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             }
         }
         lslot = lslot == D - 1 ? 0 : lslot + 1;
+    };
+    auto issue = [&]() __attribute__((always_inline)) {
+        const uint32_t base = slot_base();
+#pragma unroll
+        for (int u = 0; u < L::kXDma; ++u) dma_x(base, u);
+#pragma unroll
+        for (int b = 0; b < kSkNTW; ++b) dma_q(base, b);
+        dma_sz(base);
+        advance();
     };
 
     // ---- land: wait for the oldest stage in flight, zero its x pieces at
@@ -326,108 +333,148 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
 
     // ---- main loop: segments of one tile, one stage per inner trip ----
     // The epilogue sits outside the stage loop, so the accumulators stay in
-    // the MFMA registers across stages.
-    int cslot = 0, cst = i0 - t * p.ST;
+    // the MFMA registers across stages.  A stage is: the head (DMA issue of
+    // stage + 2, the stage's raw weights, scales and zero points, step 0's x
+    // fragments and dequant), steps 0..5 (MFMAs of step s while step s + 1's
+    // operands are read and dequantized), the operands of steps 6 and 7 read
+    // into registers, the barrier that lands the next stage, and then the
+    // MFMAs of steps 6 and 7 issued together with the next stage's head, so
+    // the matrix core keeps running through the barrier while the DMA issue
+    // and the next stage's LDS reads are in flight.  Nothing reads a slot
+    // after the barrier that follows its last stage, so the DMA that the next
+    // head issues into it is safe.
+    //
+    // B fragment f covers local n-tiles 4 wave + 2 f + {0, 1}; lane (c32, h)
+    // needs, at 16-k step s, the 8 nibbles of row c32 % 16 of tile c32 / 16 at
+    // k-group 2 s + h: word s / 2 of tile lane ((2 s + h) % 4) * 16 + c32 % 16.
+    // Two 16-byte reads per fragment hold all of them: qb[f][0] for even s,
+    // qb[f][1] for odd s.
+    u32x4_t qb[kSkFN][2];
+    ScaleT sc[kSkFN][SPS];
+    uint32_t zb[kSkFN];
+    auto load_stage = [&](int slot) __attribute__((always_inline)) {
+        const unsigned char *sl = ring[slot];
+#pragma unroll
+        for (int f = 0; f < kSkFN; ++f) {
+            const int ntl = wave * kSkNTW + 2 * f + (c32 >> 4);
+            const unsigned char *qt = sl + L::kQ + ntl * kTileBytes;
+            qb[f][0] = *(const u32x4_t *)(qt + (h * 16 + (c32 & 15)) * 16);
+            qb[f][1] = *(const u32x4_t *)(qt + ((2 + h) * 16 + (c32 & 15)) * 16);
+            const ScaleT *sp = (const ScaleT *)(sl + L::kS + ntl * L::kTileS) + (c32 & 15) * SPS;
+#pragma unroll
+            for (int e = 0; e < SPS; ++e) sc[f][e] = sp[e];
+            if constexpr (HAS_ZP) {
+                const unsigned char *zp = sl + L::kZ + ntl * L::kTileZ + (c32 & 15) * ZB;
+                uint32_t z = 0;
+#pragma unroll
+                for (int e = 0; e < ZB; ++e) z |= (uint32_t)zp[e] << (8 * e);
+                zb[f] = z;
+            } else {
+                zb[f] = 0x88888888u;
+            }
+        }
+    };
+    auto read_x = [&](half8_t(&af)[kSkFM], int slot, int s) __attribute__((always_inline)) {
+        // row a * 32 + c32 (row & 15 == c32 & 15), k-chunk 2 s + h
+        const _Float16 *xs = (const _Float16 *)(ring[slot] + L::kX);
+#pragma unroll
+        for (int a = 0; a < kSkFM; ++a)
+            af[a] = *(const half8_t *)(xs + (a * 32 + c32) * kTileK + (((2 * s + h) ^ (c32 & 15)) * 8));
+    };
+    auto dequant = [&](half8_t(&bf)[kSkFN], int s) __attribute__((always_inline)) {
+        const int si = s * SPS / 8;   // scale block of k-group 2 s + h (same for both h)
+#pragma unroll
+        for (int f = 0; f < kSkFN; ++f) {
+            const uint32_t z = HAS_ZP ? zp_nibble(zb[f], si) : 8u;
+            half8_t w = unpack_q_minus_zp(qb[f][s & 1][s >> 1], bias_lo_pair(z), bias_hi_pair(z), k6400);
+            if constexpr (sizeof(ScaleT) == 2) {
+                w = w * (_Float16)sc[f][si];
+            } else {
+                const float sf = (float)sc[f][si];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) w[e] = (_Float16)((float)w[e] * sf);
+            }
+            bf[f] = w;
+        }
+    };
+    auto mfma_step = [&](const half8_t(&af)[kSkFM], const half8_t(&bf)[kSkFN]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int a = 0; a < kSkFM; ++a)
+#pragma unroll
+            for (int f = 0; f < kSkFN; ++f) acc[a][f] = mfma32x32x16(bf[f], af[a], acc[a][f]);
+    };
+    int cslot = 0, cst = i0 - t * p.ST;      // ring slot and stage (within its tile) being computed
+    constexpr int kSteps = kTileK / 16;      // 8 MFMA k-steps per stage
+    half8_t af[2][kSkFM], bf[2][kSkFN];      // steps 0..6, alternating
+    half8_t af7[kSkFM], bf7[kSkFN];          // step 7, held across the barrier
+    auto head_reads = [&]() __attribute__((always_inline)) {
+        load_stage(cslot);
+        read_x(af[0], cslot, 0);
+        dequant(bf[0], 0);
+    };
     int remaining = i1 - i0;
     int seg_n = min(remaining, p.ST - cst);   // stages of tile t done by this workgroup
+    issue();                                   // stages 0 and 1 (three-slot ring: and 2)
     issue();
-    if (D == 3) issue();
     land(0, cst);
+    if (D == 3) issue();
+    head_reads();
+    int kk = 0;                                // stages of the current segment done
     while (true) {
-        for (int kk = 0; kk < seg_n; ++kk) {
-            issue();   // stage + 2 (three-slot ring) or stage + 1 (two slots)
-            const unsigned char *sl = ring[cslot];
-            // B fragment f covers local n-tiles 4 wave + 2 f + {0, 1}; lane
-            // (c32, h) needs, at 16-k step s, the 8 nibbles of row c32 % 16 of
-            // tile c32 / 16 at k-group 2 s + h: word s / 2 of tile lane
-            // ((2 s + h) % 4) * 16 + c32 % 16.  Two 16-byte reads per fragment
-            // hold all of them: qb[f][0] for even s, qb[f][1] for odd s.
-            u32x4_t qb[kSkFN][2];
-            ScaleT sc[kSkFN][SPS];
-            uint32_t zb[kSkFN];
 #pragma unroll
-            for (int f = 0; f < kSkFN; ++f) {
-                const int ntl = wave * kSkNTW + 2 * f + (c32 >> 4);
-                const unsigned char *qt = sl + L::kQ + ntl * kTileBytes;
-                qb[f][0] = *(const u32x4_t *)(qt + (h * 16 + (c32 & 15)) * 16);
-                qb[f][1] = *(const u32x4_t *)(qt + ((2 + h) * 16 + (c32 & 15)) * 16);
-                const ScaleT *sp = (const ScaleT *)(sl + L::kS + ntl * L::kTileS) + (c32 & 15) * SPS;
+        for (int s = 0; s + 2 < kSteps; ++s) {
+            read_x(af[(s + 1) & 1], cslot, s + 1);
+            dequant(bf[(s + 1) & 1], s + 1);
+            mfma_step(af[s & 1], bf[s & 1]);
+            // order within the step: the next step's x reads go out first,
+            // between the MFMAs, and its dequant VALU fills the MFMA shadow
 #pragma unroll
-                for (int e = 0; e < SPS; ++e) sc[f][e] = sp[e];
-                if constexpr (HAS_ZP) {
-                    const unsigned char *zp = sl + L::kZ + ntl * L::kTileZ + (c32 & 15) * ZB;
-                    uint32_t z = 0;
-#pragma unroll
-                    for (int e = 0; e < ZB; ++e) z |= (uint32_t)zp[e] << (8 * e);
-                    zb[f] = z;
-                } else {
-                    zb[f] = 0x88888888u;
-                }
+            for (int i = 0; i < kSkFM; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // VALU
             }
-            const _Float16 *xs = (const _Float16 *)(sl + L::kX);
-            auto read_x = [&](half8_t(&af)[kSkFM], int s) __attribute__((always_inline)) {
-                // row a * 32 + c32 (row & 15 == c32 & 15), k-chunk 2 s + h
 #pragma unroll
-                for (int a = 0; a < kSkFM; ++a)
-                    af[a] = *(const half8_t *)(xs + (a * 32 + c32) * kTileK + (((2 * s + h) ^ (c32 & 15)) * 8));
-            };
-            auto dequant = [&](half8_t(&bf)[kSkFN], int s) __attribute__((always_inline)) {
-                const int si = s * SPS / 8;   // scale block of k-group 2 s + h (same for both h)
+            for (int i = 0; i < kSkFM * kSkFN - kSkFM; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // af[0], bf[0] hold step 6; step 7 goes to its own registers
+        read_x(af7, cslot, kSteps - 1);
+        dequant(bf7, kSteps - 1);
+        cslot = cslot == D - 1 ? 0 : cslot + 1;
+        cst = cst + 1 == p.ST ? 0 : cst + 1;
+        land(cslot, cst);   // after the last stage this waits for re-loads nobody reads
+        // MFMAs of steps 6 and 7 with the DMA of a later stage between them,
+        // then the next stage's head (at the end of the range these load and
+        // read stages nobody uses: the issue cursor stays on the last one)
+        {
+            const uint32_t base = slot_base();
+            static_assert(L::kXDma + kSkNTW < 2 * kSkFM * kSkFN, "one DMA per tail MFMA");
 #pragma unroll
-                for (int f = 0; f < kSkFN; ++f) {
-                    const uint32_t z = HAS_ZP ? zp_nibble(zb[f], si) : 8u;
-                    half8_t w = unpack_q_minus_zp(qb[f][s & 1][s >> 1], bias_lo_pair(z), bias_hi_pair(z), k6400);
-                    if constexpr (sizeof(ScaleT) == 2) {
-                        w = w * (_Float16)sc[f][si];
-                    } else {
-                        const float sf = (float)sc[f][si];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) w[e] = (_Float16)((float)w[e] * sf);
-                    }
-                    bf[f] = w;
-                }
-            };
-            // step s + 1's x fragments are read and its weights dequantized while
-            // the MFMAs of step s run
-            half8_t af[2][kSkFM], bf[2][kSkFN];
-            read_x(af[0], 0);
-            dequant(bf[0], 0);
-#pragma unroll
-            for (int s = 0; s < kTileK / 16; ++s) {
-                if (s + 1 < kTileK / 16) {
-                    read_x(af[(s + 1) & 1], s + 1);
-                    dequant(bf[(s + 1) & 1], s + 1);
-                }
-#pragma unroll
-                for (int a = 0; a < kSkFM; ++a)
-#pragma unroll
-                    for (int f = 0; f < kSkFN; ++f) acc[a][f] = mfma32x32x16(bf[s & 1][f], af[s & 1][a], acc[a][f]);
-                // order within the step: the next step's x reads go out first,
-                // between the MFMAs, and its dequant VALU fills the MFMA shadow
-                if (s + 1 < kTileK / 16) {
-#pragma unroll
-                    for (int i = 0; i < kSkFM; ++i) {
-                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // VALU
-                    }
-#pragma unroll
-                    for (int i = 0; i < kSkFM * kSkFN - kSkFM; ++i) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
-                    }
-                }
+            for (int i = 0; i < 2 * kSkFM * kSkFN; ++i) {
+                const int a = (i / kSkFN) % kSkFM, f = i % kSkFN;
+                if (i < kSkFM * kSkFN) acc[a][f] = mfma32x32x16(bf[0][f], af[0][a], acc[a][f]);
+                else acc[a][f] = mfma32x32x16(bf7[f], af7[a], acc[a][f]);
+                __builtin_amdgcn_sched_barrier(0);
+                if (i < L::kXDma) dma_x(base, i);
+                else if (i < L::kXDma + kSkNTW) dma_q(base, i - L::kXDma);
+                else if (i == L::kXDma + kSkNTW) dma_sz(base);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            cslot = cslot == D - 1 ? 0 : cslot + 1;
-            cst = cst + 1 == p.ST ? 0 : cst + 1;
-            land(cslot, cst);   // after the last stage this waits for re-loads nobody reads
         }
-        remaining -= seg_n;
-        epilogue(seg_n);
-        if (remaining == 0) break;
-        ++t;
-        seg_n = min(remaining, p.ST);
+        advance();
+        head_reads();
+        if (++kk == seg_n) {
+            remaining -= seg_n;
+            epilogue(seg_n);
+            if (remaining == 0) break;
+            ++t;
+            seg_n = min(remaining, p.ST);
+            kk = 0;
+        }
     }
     // drain every direct load before the workgroup's LDS is released
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
