@@ -61,7 +61,7 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
 #pragma unroll
         for (int t = 0; t < STW; ++t) {
             const int st = min(c * STW + t, p.ST - 1);
-            raw[t] = qp[(size_t)st * 64];
+            raw[t] = gld_nt(qp + (size_t)st * 64);
             load_scale_row<ScaleT, SPS>(sp + (size_t)st * kTileRows * SPS, sv[t]);
             if constexpr (HAS_ZP) zb[t] = load_zp<ZB>(zpp + (size_t)st * kTileRows * ZB);
             else zb[t] = 0x88888888u;

@@ -84,7 +84,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
     // tile, which is never computed), so the loop below has a fixed number of
     // loads in flight and exact wait counts.
     auto issue = [&](int d) {
-        raw[d] = gld(iref.q + (size_t)ist * 64);
+        raw[d] = gld_nt(iref.q + (size_t)ist * 64);
         load_scale_row<ScaleT, SPS>(iref.s + (size_t)ist * kTileRows * SPS, sv[d]);
         if constexpr (HAS_ZP) zb[d] = load_zp<ZB>(iref.z + (size_t)ist * kTileRows * ZB);
         else zb[d] = 0x88888888u;
