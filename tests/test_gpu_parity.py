@@ -287,6 +287,32 @@ def test_gemm_determinism_tiling_and_pow2_scaling(ctx):
     w.close()
 
 
+def test_tall_single_row_product(ctx):
+    """A tall M = 1 product (4376 n-tiles, more than the chip holds waves):
+    N = 70001 leaves a partial last n-tile, K = 1000 a k tail inside a
+    super-tile; zero points, fp16 and fp32 outputs, y += and row 0 of an M = 2
+    product (the 16-row kernel variant) all agree."""
+    N, K = 70001, 1000
+    t = synth.make_weight(61, N, K, 32, with_zp=True)
+    w = upload(ctx, t)
+    try:
+        x2 = synth.make_x(62, 2, K)
+        x16 = np.ascontiguousarray(x2[:1])
+        y_ref, _ = oracle_matmul(t, x16)
+        y32 = w.matmul(x16[0])
+        assert_parity(y32.reshape(1, N), y_ref, x16, t, None, False, "tall M=1")
+        y16 = w.matmul(x16[0], out_dtype=np.float16)
+        assert np.array_equal(y16.view(np.uint16), y32.astype(np.float16).view(np.uint16))
+        y0 = np.random.default_rng(63).standard_normal(N).astype(np.float32)
+        acc = w.matmul(x16[0], y=y0.copy(), accumulate=True)
+        assert np.array_equal(acc.view(np.uint32), (y0 + y32).view(np.uint32))
+        y_pair = w.matmul(x2)
+        tol = 1e-3 * np.sqrt(K) * float(np.abs(x16.astype(np.float32)).max()) * max_abs_w(t)
+        assert float(np.abs(y_pair[0] - y32).max()) <= tol
+    finally:
+        w.close()
+
+
 @pytest.mark.parametrize("M,K,N", [(200, 3072, 1000), (300, 4096, 1001), (130, 8192, 3072)])
 def test_gemm_split_tiles_tails_and_outputs(ctx, M, K, N):
     """Few tiles, so stream-K splits them across workgroups and the partial
