@@ -212,10 +212,14 @@ int32_t mnb_max_batch_rows(void);
  * submissions of Phi3GpuPipeline.java:191-231): the items may run
  * concurrently, so no item may read another item's output.
  * Each item: device pointers, fp16 x [M, K] (K a multiple of 8, 16-byte
- * aligned), y [M, N] fp16 or fp32, 1 <= M <= 16; all items share the weight
- * variant (scale type, zero points or not, block size class) and either all
- * have M == 1 or all have M > 1.  The group keeps its own device descriptor
- * table, so mnb_group_run allocates nothing and can be captured in a HIP graph. */
+ * aligned), y [M, N] fp16 or fp32, M >= 1; all items share the weight variant
+ * (scale type, zero points or not, block size class) and one M class: all
+ * M == 1 (one persistent streaming launch), all 1 < M <= 16, or all M > 16
+ * (prefill-shaped products: one stream-K GEMM launch over all items'
+ * tiles, plus its split-tile reduce, using the context's GEMM workspace, so
+ * it must not overlap other M > 16 calls on the context).  The group keeps
+ * its own device descriptor table, so mnb_group_run allocates nothing and can
+ * be captured in a HIP graph. */
 typedef struct mnb_group mnb_group;
 typedef struct mnb_group_item {
     const mnb_weight *weight;

@@ -475,3 +475,60 @@ def test_group_matches_oracle_and_single_launches(ctx):
                                          torch.zeros((2, 3072), dtype=torch.float16, device="cuda"))])
     for w, _, _ in entries:
         w.close()
+
+
+def test_group_of_prefill_products(ctx):
+    """Independent products with M > 16 recorded as one group: one stream-K
+    launch whose workgroup ranges run across item boundaries (different K, so
+    different stage counts per tile; M and N tails; fp16 and fp32 outputs;
+    y +=).  Every item is within the tolerance of the oracle on sampled rows,
+    within the tolerance of its own single launch, and replays are bitwise
+    identical."""
+    import torch
+    specs = [(200, 3072, 1000, np.float16, False), (64, 8192, 3072, np.float32, False),
+             (512, 3072, 9216, np.float16, False), (33, 1536, 577, np.float32, True),
+             (300, 576, 1536, np.float16, False)]
+    entries, host = [], []
+    st = torch.cuda.Stream()
+    for i, (M, K, N, ydt, acc) in enumerate(specs):
+        t = synth.make_weight(1200 + i, N, K, 32, with_zp=True)
+        w = upload(ctx, t)
+        x16 = synth.make_x(1300 + i, M, K)
+        y0 = np.random.default_rng(1400 + i).standard_normal((M, N)).astype(ydt)
+        entries.append((w, torch.from_numpy(x16).cuda(), torch.from_numpy(y0.copy()).cuda()))
+        host.append((t, x16, y0, acc))
+    torch.cuda.synchronize()
+    for acc_group in (False, True):
+        items = [e for e, h in zip(entries, host) if h[3] == acc_group]
+        if not items:
+            continue
+        g = mnb_hip.Group(ctx, items, accumulate=acc_group)
+        outs = []
+        for rep in range(3):
+            with torch.cuda.stream(st):
+                for (w, xd, yd), (t, x16, y0, acc) in zip(entries, host):
+                    if acc == acc_group:
+                        yd.copy_(torch.from_numpy(y0).cuda())
+                g.run(st.cuda_stream)
+            torch.cuda.synchronize()
+            outs.append([yd.cpu().numpy().copy() for (w, xd, yd) in items])
+        for r in outs[1:]:
+            for a, b in zip(outs[0], r):
+                assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
+        hs = [h for h in host if h[3] == acc_group]
+        for (w, xd, yd), (t, x16, y0, acc), y in zip(items, hs, outs[0]):
+            rows = np.sort(np.random.default_rng(t.N).choice(t.N, min(t.N, 512), replace=False))
+            y_ref, _ = oracle_matmul(t, x16, rows)
+            base = y0.astype(np.float32)[:, rows] if acc else 0.0
+            label = "group M=%d K=%d N=%d acc=%d" % (x16.shape[0], t.K, t.N, acc)
+            assert_parity(y.astype(np.float32)[:, rows] - base, y_ref, x16, t, None, y.dtype == np.float16, label)
+            single = w.matmul(x16, y=y0.astype(np.float32).copy() if acc else None, accumulate=acc)
+            tol = 1e-3 * np.sqrt(t.K) * float(np.abs(x16.astype(np.float32)).max()) * max_abs_w(t)
+            err = np.abs(single - y.astype(np.float32))
+            assert float(np.max(err - (fp16_ulp(single) if y.dtype == np.float16 else 0.0))) <= tol, label
+        g.close()
+    with pytest.raises(mnb_hip.MnbError):       # M <= 16 and M > 16 do not mix
+        mnb_hip.Group(ctx, [entries[0], (entries[1][0], torch.zeros((2, 8192), dtype=torch.float16, device="cuda"),
+                                         torch.zeros((2, 3072), dtype=torch.float32, device="cuda"))])
+    for w, _, _ in entries:
+        w.close()

@@ -682,8 +682,62 @@ int32_t mnb_dequantize(mnb_context *ctx, const mnb_weight *w, void *out, int32_t
 
 struct mnb_group {
     mnb_context *ctx = nullptr;
-    mnb::GemvGroupPlan plan;
+    mnb::GemvGroupPlan plan;        // items with M <= 16
+    bool gemm = false;              // items with M > 16: one stream-K GEMM launch
+    mnb::GemmGroupPlan gplan;
 };
+
+// A group of products with M > 16: the items' (tile, stage) iterations in
+// group order, one stream-K launch over one workgroup per CU (the iterations
+// of a whole group far exceed the CU count).
+static int32_t group_create_gemm(mnb_context *ctx, int32_t count, const mnb_group_item *items, mnb_group **out) {
+    mnb::GemmGroupPlan plan;
+    plan.host.resize((size_t)count);
+    int64_t iters = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        const mnb_group_item &it = items[i];
+        const mnb_weight *w = it.weight;
+        const WeightGeom &g = w->g;
+        if (i == 0) {
+            plan.scale_f32 = g.scale_f32;
+            plan.has_zp = g.has_zp;
+            plan.sps = g.SPS;
+        } else if (plan.scale_f32 != g.scale_f32 || plan.has_zp != g.has_zp || plan.sps != g.SPS) {
+            return fail(MNB_ERR_UNSUPPORTED, "item %d: a group needs one weight variant and one M class", i);
+        }
+        if ((int64_t)it.M * g.K * 2 >= ((int64_t)1 << 31) || (uint64_t)g.NT * (uint64_t)g.ST * mnb::kTileBytes >= ((uint64_t)1 << 32))
+            return fail(MNB_ERR_UNSUPPORTED, "item %d: x of 2 GiB or packed weights of 4 GiB or more in a group", i);
+        mnb::MatmulArgs a;
+        a.x = (const _Float16 *)it.x;
+        a.ldx = g.K;
+        a.kx = g.K;
+        a.M = it.M;
+        a.y = it.y;
+        a.y_type = it.y_type;
+        a.accumulate = (it.flags & MNB_ACCUMULATE) ? 1 : 0;
+        plan.host[(size_t)i] = mnb::sk_make_item(w, a, (int32_t)std::min<int64_t>(iters, INT32_MAX));
+        iters += (int64_t)plan.host[(size_t)i].T * g.ST;
+        if (iters >= ((int64_t)1 << 31)) return fail(MNB_ERR_INVALID_ARGUMENT, "group too large");
+    }
+    plan.count = count;
+    plan.iters = iters;
+    plan.G = (int32_t)std::min<int64_t>(std::min(ctx->cu_count, 256), iters);
+    DeviceGuard guard(ctx->device);
+    hipError_t e;
+    if ((e = dev_alloc(&plan.items, plan.host.size() * sizeof(mnb::SkItem))) != hipSuccess ||
+        (e = hipMemcpy(plan.items, plan.host.data(), plan.host.size() * sizeof(mnb::SkItem), hipMemcpyHostToDevice)) !=
+            hipSuccess) {
+        if (plan.items) (void)hipFree(plan.items);
+        return hip_fail(e, "group");
+    }
+    mnb_group *grp = new mnb_group();
+    grp->ctx = ctx;
+    grp->gemm = true;
+    grp->gplan = std::move(plan);
+    ctx->live_weights++;   // a group keeps its context alive like a weight does
+    *out = grp;
+    return ok();
+}
 
 extern "C" {
 
@@ -701,8 +755,9 @@ int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *
         if (!w) return fail(MNB_ERR_INVALID_STATE, "item %d: Kernel not prepared", i);
         if (w->ctx != ctx) return fail(MNB_ERR_INVALID_ARGUMENT, "item %d: weight belongs to another context", i);
         const WeightGeom &g = w->g;
-        if (it.M < 1 || it.M > mnb::kSkinnyMaxM)
-            return fail(MNB_ERR_UNSUPPORTED, "item %d: M=%d; group items take 1 <= M <= %d", i, it.M, mnb::kSkinnyMaxM);
+        if (it.M < 1) return fail(MNB_ERR_INVALID_ARGUMENT, "item %d: M=%d must be at least 1", i, it.M);
+        if ((it.M > mnb::kSkinnyMaxM) != (items[0].M > mnb::kSkinnyMaxM))
+            return fail(MNB_ERR_UNSUPPORTED, "item %d: a group needs one weight variant and one M class", i);
         if (it.x_type != MNB_F16 || (g.K % 8) != 0 || ((uintptr_t)it.x & 15u) || !it.x)
             return fail(MNB_ERR_UNSUPPORTED, "item %d: x must be 16-byte aligned fp16 with K a multiple of 8", i);
         if ((it.y_type != MNB_F16 && it.y_type != MNB_F32) || !it.y)
@@ -738,6 +793,7 @@ int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *
         if (waves > 16) waves = 16;
         if (waves > plan.waves) plan.waves = waves;
     }
+    if (items[0].M > mnb::kSkinnyMaxM) return group_create_gemm(ctx, count, items, out);
     if (wgs > std::numeric_limits<int32_t>::max()) return fail(MNB_ERR_INVALID_ARGUMENT, "group too large");
     std::vector<uint16_t> wg_item((size_t)wgs);
     for (int32_t i = 0; i < count; ++i) {
@@ -826,6 +882,11 @@ int32_t mnb_group_run(mnb_context *ctx, const mnb_group *group, void *stream) {
     if (group->ctx != ctx) return fail(MNB_ERR_INVALID_ARGUMENT, "group belongs to another context");
     DeviceGuard guard(ctx->device);
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
+    if (group->gemm) {
+        const hipError_t e = mnb::launch_gemm_group(group->gplan, (float *)ctx->sk_ws, s);
+        if (e != hipSuccess) return hip_fail(e, "matmulBatch");
+        return ok();
+    }
     hipError_t e = group->plan.m1 ? mnb::launch_gemv_stream(group->plan, s) : mnb::launch_gemv_group(group->plan, s);
     if (e != hipSuccess) return hip_fail(e, "matvec");
     return ok();
@@ -835,8 +896,9 @@ int32_t mnb_group_destroy(mnb_group *group) {
     if (!group) return ok();
     DeviceGuard guard(group->ctx->device);
     hipError_t first = hipStreamSynchronize(group->ctx->stream), e;
-    if ((e = hipFree(group->plan.items)) != hipSuccess && first == hipSuccess) first = e;
-    if ((e = hipFree(group->plan.wg_item)) != hipSuccess && first == hipSuccess) first = e;
+    if (group->gplan.items && (e = hipFree(group->gplan.items)) != hipSuccess && first == hipSuccess) first = e;
+    if (group->plan.items && (e = hipFree(group->plan.items)) != hipSuccess && first == hipSuccess) first = e;
+    if (group->plan.wg_item && (e = hipFree(group->plan.wg_item)) != hipSuccess && first == hipSuccess) first = e;
     if (group->plan.units && (e = hipFree(group->plan.units)) != hipSuccess && first == hipSuccess) first = e;
     if (group->plan.wave_begin && (e = hipFree(group->plan.wave_begin)) != hipSuccess && first == hipSuccess) first = e;
     group->ctx->live_weights--;

@@ -24,8 +24,11 @@
 // fragment reads are free of bank conflicts.
 //
 // Stream-K: the grid is one persistent workgroup per CU.  The (tile, stage)
-// iterations of the whole product are cut into equal contiguous ranges, one
+// iterations of the whole launch are cut into equal contiguous ranges, one
 // per workgroup, so every CU gets the same MFMA work whatever the tile count.
+// A launch covers one product (mnb_matmul) or a recorded group of
+// independent products (mnb_group_*, M > 16): the items' iterations follow
+// one another, and a workgroup's range may run from one item into the next.
 // A workgroup that owns all stages of a tile writes y directly.  A tile whose
 // stages span several workgroups is written as fp32 partial tiles, one per
 // contributor, and summed in contributor order by sk_reduce_kernel, launched
@@ -56,19 +59,42 @@ __device__ __forceinline__ float16_t mfma32x32x16(half8_t a, half8_t b, float16_
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// The launch's parameters: its items and the stream-K split.
 struct SkParams {
-    const u32x4_t *q_t;
-    const void *s_t;
-    const uint8_t *zp_t;
-    const _Float16 *x;
-    int32_t ldx, kx, M, N, NT, ST;
-    void *y;
-    int32_t y_f16, accumulate;
-    int32_t y_vec;          // N % 4 == 0 and y aligned for 4-element stores
-    int32_t MT, T, G;       // m-tiles, tiles, workgroups
-    int32_t I;              // iterations = T * ST (below 2^31)
+    SkItem one;             // the item when count == 1 (a single product)
+    const SkItem *items;    // device table of count items (count > 1), ibeg ascending
+    int32_t count;
+    int32_t G;              // workgroups
+    int32_t I;              // iterations of all items (below 2^31)
     float *ws;              // [G][2] partial tiles: slot 0 for a workgroup's first tile, 1 for its last
 };
+
+// Item i (uniform index).  The table is read through the constant address
+// space: it is never written by the kernel, so these are scalar loads and the
+// fields stay in scalar registers.
+__device__ __forceinline__ SkItem sk_item(const SkParams &p, int i) {
+    if (p.count == 1) return p.one;
+    static_assert(sizeof(SkItem) % 4 == 0, "dword copy");
+    const __attribute__((address_space(4))) uint32_t *src =
+        (const __attribute__((address_space(4))) uint32_t *)(p.items + i);
+    SkItem r;
+    uint32_t *dst = (uint32_t *)&r;
+#pragma unroll
+    for (int k = 0; k < (int)(sizeof(SkItem) / 4); ++k) dst[k] = src[k];
+    return r;
+}
+
+// Item that owns iteration i (binary search over the items' first iterations).
+__device__ __forceinline__ int sk_find_item(const SkParams &p, int i) {
+    if (p.count == 1) return 0;
+    int lo = 0, hi = p.count - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (((const __attribute__((address_space(4))) SkItem *)p.items)[mid].ibeg <= i) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
 
 // first iteration of logical workgroup g (g = G gives I)
 __device__ __forceinline__ int sk_start(int g, const SkParams &p) { return (int)((int64_t)g * p.I / p.G); }
@@ -84,7 +110,7 @@ __device__ __forceinline__ int sk_owner(int i, const SkParams &p) {
 // Four consecutive outputs y[m, n..n+3] (=|+=) v, m < M checked by the
 // caller; columns >= N are dropped.  One 8-byte (fp16) or 16-byte (fp32)
 // store when the row segment is whole and aligned.
-__device__ __forceinline__ void store_y4(const SkParams &p, int m, int n, float4_t v) {
+__device__ __forceinline__ void store_y4(const SkItem &p, int m, int n, float4_t v) {
     const size_t idx = (size_t)m * p.N + n;
     const bool acc = p.accumulate != 0;
     if (p.y_vec && n + 3 < p.N) {
@@ -130,7 +156,16 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 // inline asm, so the compiler neither tracks it nor moves memory accesses
 // across it; the kernel waits for it explicitly.
 __device__ __forceinline__ void dma16(uint32_t m0, uint32_t off, const void *base) {
-    asm volatile("global_load_lds_dwordx4 %1, %2" ::"{m0}"(m0), "v"(off), "s"(base) : "memory");
+    // the base is wave-uniform (it comes from the item tables); make that
+    // explicit so it is held in scalar registers.  The builtin returns a
+    // signed int: each half goes back through uint32_t, so the low dword is
+    // zero-extended (a sign extension would set the high dword to all ones
+    // whenever bit 31 of the address is set).
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+    const uint64_t u = (uint64_t)lo | ((uint64_t)hi << 32);
+    asm volatile("global_load_lds_dwordx4 %1, %2" ::"{m0}"(m0), "v"(off), "s"((const void *)(uintptr_t)u) : "memory");
 }
 
 // Ring slot layout (bytes) for one stage, and the direct loads that fill it.
@@ -174,6 +209,11 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     const int g = (p.G % 8 == 0) ? (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8) : (int)blockIdx.x;
     const int i0 = sk_start(g, p), i1 = sk_start(g + 1, p);
     if (i0 >= i1) return;
+    // compute cursor: item ci (fields ic), tile t of the item, stage cst of the tile
+    int ci = sk_find_item(p, i0);
+    SkItem ic = sk_item(p, ci);
+    int t = (i0 - ic.ibeg) / ic.ST;
+    int cst = (i0 - ic.ibeg) - t * ic.ST;
 
     const uint32_t k6400 = vgpr_const(0x64006400u);
     const uint32_t ring0 = __builtin_amdgcn_readfirstlane(lds_addr(&ring[0][0]));
@@ -193,27 +233,29 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     constexpr int z_win_max = L::kZRegion - L::kWin;
     const int s_win = min(wave * kSkNTW * L::kTileS, s_win_max);
     const int z_win = HAS_ZP ? min(wave * kSkNTW * L::kTileZ, z_win_max) : 0;
-    int lt = i0 / p.ST, lst = i0 - lt * p.ST, li = i0, lslot = 0;
+    // issue cursor: item ii (fields iq), tile lt, stage lst, iteration li
+    int ii = ci, lt = t, lst = cst, li = i0, lslot = 0;
+    SkItem iq = ic;
     uint32_t xrow[L::kXDma], xcolk[L::kXDma], qoff[kSkNTW], soff = 0, zoff = 0;
     auto set_tile = [&]() __attribute__((always_inline)) {
-        const int m0 = (lt % p.MT) * kSkBM, ntg = (lt / p.MT) * L::kNT, nt0 = ntg + wave * kSkNTW;
+        const int m0 = (lt % iq.MT) * kSkBM, ntg = (lt / iq.MT) * L::kNT, nt0 = ntg + wave * kSkNTW;
 #pragma unroll
         for (int u = 0; u < L::kXDma; ++u) {
             const int row = (wave * L::kXDma + u) * 4 + (lane >> 4);
-            xrow[u] = (uint32_t)min(m0 + row, p.M - 1) * (uint32_t)p.ldx * 2u;
+            xrow[u] = (uint32_t)min(m0 + row, iq.M - 1) * (uint32_t)iq.ldx * 2u;
             xcolk[u] = (uint32_t)(((lane & 15) ^ (row & 15)) * 8);   // k of the chunk this lane loads
         }
 #pragma unroll
         for (int b = 0; b < kSkNTW; ++b)
-            qoff[b] = ((uint32_t)min(nt0 + b, p.NT - 1) * (uint32_t)p.ST * 64u + (uint32_t)lane) * 16u;
+            qoff[b] = ((uint32_t)min(nt0 + b, iq.NT - 1) * (uint32_t)iq.ST * 64u + (uint32_t)lane) * 16u;
         {
             const int byte = s_win + lane * 16;
-            soff = (uint32_t)min(ntg + byte / L::kTileS, p.NT - 1) * (uint32_t)p.ST * L::kTileS +
+            soff = (uint32_t)min(ntg + byte / L::kTileS, iq.NT - 1) * (uint32_t)iq.ST * L::kTileS +
                    (uint32_t)(byte % L::kTileS);
         }
         if constexpr (HAS_ZP) {
             const int byte = z_win + lane * 16;
-            zoff = (uint32_t)min(ntg + byte / L::kTileZ, p.NT - 1) * (uint32_t)p.ST * L::kTileZ +
+            zoff = (uint32_t)min(ntg + byte / L::kTileZ, iq.NT - 1) * (uint32_t)iq.ST * L::kTileZ +
                    (uint32_t)(byte % L::kTileZ);
         }
     };
@@ -221,24 +263,27 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     // x piece u of this wave (4 rows); chunks at k >= kx (a k tail) re-read
     // the row's last chunk, stay inside x, and are zeroed in LDS on landing
     auto dma_x = [&](uint32_t base, int u) __attribute__((always_inline)) {
-        const uint32_t k = (uint32_t)min(lst * kTileK + (int)xcolk[u], p.kx - 8);
-        dma16(base + L::kX + (uint32_t)(wave * L::kXDma + u) * 1024u, xrow[u] + k * 2u, p.x);
+        const uint32_t k = (uint32_t)min(lst * kTileK + (int)xcolk[u], iq.kx - 8);
+        dma16(base + L::kX + (uint32_t)(wave * L::kXDma + u) * 1024u, xrow[u] + k * 2u, iq.x);
     };
     auto dma_q = [&](uint32_t base, int b) __attribute__((always_inline)) {
-        const unsigned char *qb = (const unsigned char *)p.q_t + (size_t)lst * kTileBytes;
+        const unsigned char *qb = (const unsigned char *)iq.q_t + (size_t)lst * kTileBytes;
         dma16(base + L::kQ + (uint32_t)(wave * kSkNTW + b) * kTileBytes, qoff[b], qb);
     };
     auto dma_sz = [&](uint32_t base) __attribute__((always_inline)) {
-        dma16(base + L::kS + (uint32_t)s_win, soff, (const unsigned char *)p.s_t + (size_t)lst * L::kTileS);
-        if constexpr (HAS_ZP) dma16(base + L::kZ + (uint32_t)z_win, zoff, p.zp_t + (size_t)lst * L::kTileZ);
+        dma16(base + L::kS + (uint32_t)s_win, soff, (const unsigned char *)iq.s_t + (size_t)lst * L::kTileS);
+        if constexpr (HAS_ZP) dma16(base + L::kZ + (uint32_t)z_win, zoff, iq.zp_t + (size_t)lst * L::kTileZ);
     };
     auto slot_base = [&]() __attribute__((always_inline)) { return ring0 + (uint32_t)(lslot * L::kBytes); };
     auto advance = [&]() __attribute__((always_inline)) {
         if (li + 1 < i1) {
             ++li;
-            if (++lst == p.ST) {
+            if (++lst == iq.ST) {
                 lst = 0;
-                ++lt;
+                if (++lt == iq.T) {
+                    lt = 0;
+                    iq = sk_item(p, ++ii);
+                }
                 set_tile();
             }
         }
@@ -257,20 +302,20 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     // ---- land: wait for the oldest stage in flight, zero its x pieces at
     // k >= kx, and meet the other waves ----
     bool drain = false;   // set after y stores: stores and loads may complete out of order
-    auto land = [&](int slot, int st) __attribute__((always_inline)) {
+    auto land = [&](int slot, int st, int kx) __attribute__((always_inline)) {
         if (drain || D == 2) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             drain = false;
         } else {
             asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L::kDma) : "memory");   // only the newest stage in flight
         }
-        if ((st + 1) * kTileK > p.kx) {
+        if ((st + 1) * kTileK > kx) {
             unsigned char *xs = &ring[slot][L::kX];
 #pragma unroll
             for (int u = 0; u < L::kXDma; ++u) {
                 const int row = (wave * L::kXDma + u) * 4 + (lane >> 4);
                 const int chunk = (lane & 15) ^ (row & 15);
-                if (st * kTileK + chunk * 8 >= p.kx)
+                if (st * kTileK + chunk * 8 >= kx)
                     *(u32x4_t *)(xs + (wave * L::kXDma + u) * 1024 + lane * 16) = (u32x4_t){0u, 0u, 0u, 0u};
             }
         }
@@ -288,28 +333,27 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     // ---- epilogue of tile t after nst of its stages ----
     // Fragment (a, f), register v of lane (c32, h): row a * 32 + c32 of the
     // tile, column 32 f + 8 (v / 4) + 4 h + v % 4 of the wave's 32 columns.
-    int t = i0 / p.ST;
     auto epilogue = [&](int nst) __attribute__((always_inline)) {
-        const int m0 = (t % p.MT) * kSkBM, ng = t / p.MT;
+        const int m0 = (t % ic.MT) * kSkBM, ng = t / ic.MT;
         const int c_wave = wave * kSkNTW * kTileRows;   // first column of this wave in the tile
-        if (nst == p.ST) {
+        if (nst == ic.ST) {
             const int n_wave = ng * kSkBN + c_wave;
 #pragma unroll
             for (int a = 0; a < kSkFM; ++a) {
                 const int m = m0 + a * 32 + c32;
-                if (m < p.M) {
+                if (m < ic.M) {
 #pragma unroll
                     for (int f = 0; f < kSkFN; ++f)
 #pragma unroll
                         for (int j = 0; j < 4; ++j)
-                            store_y4(p, m, n_wave + f * 32 + 8 * j + 4 * h,
+                            store_y4(ic, m, n_wave + f * 32 + 8 * j + 4 * h,
                                      (float4_t){acc[a][f][4 * j], acc[a][f][4 * j + 1], acc[a][f][4 * j + 2],
                                                 acc[a][f][4 * j + 3]});
                 }
             }
         } else {
             // partial tile of a split tile: [kSkBM][kSkBN] fp32, summed by sk_reduce_kernel
-            const int slot = i0 / p.ST == t ? 0 : 1;   // 0 if t is this workgroup's first tile
+            const int slot = i0 >= ic.ibeg + t * ic.ST ? 0 : 1;   // 0 if t is this workgroup's first tile
             __attribute__((address_space(1))) float *part =
                 (__attribute__((address_space(1))) float *)p.ws + ((size_t)g * 2 + slot) * kSkPartialFloats;
 #pragma unroll
@@ -403,7 +447,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
 #pragma unroll
             for (int f = 0; f < kSkFN; ++f) acc[a][f] = mfma32x32x16(bf[f], af[a], acc[a][f]);
     };
-    int cslot = 0, cst = i0 - t * p.ST;      // ring slot and stage (within its tile) being computed
+    int cslot = 0;                           // ring slot of the stage being computed
     constexpr int kSteps = kTileK / 16;      // 8 MFMA k-steps per stage
     half8_t af[2][kSkFM], bf[2][kSkFN];      // steps 0..6, alternating
     half8_t af7[kSkFM], bf7[kSkFN];          // step 7, held across the barrier
@@ -413,10 +457,10 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
         dequant(bf[0], 0);
     };
     int remaining = i1 - i0;
-    int seg_n = min(remaining, p.ST - cst);   // stages of tile t done by this workgroup
+    int seg_n = min(remaining, ic.ST - cst);  // stages of tile t done by this workgroup
     issue();                                   // stages 0 and 1 (three-slot ring: and 2)
     issue();
-    land(0, cst);
+    land(0, cst, ic.kx);
     if (D == 3) issue();
     head_reads();
     int kk = 0;                                // stages of the current segment done
@@ -445,8 +489,17 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
         read_x(af7, cslot, kSteps - 1);
         dequant(bf7, kSteps - 1);
         cslot = cslot == D - 1 ? 0 : cslot + 1;
-        cst = cst + 1 == p.ST ? 0 : cst + 1;
-        land(cslot, cst);   // after the last stage this waits for re-loads nobody reads
+        // the stage to land: the next of this segment, else the first of the
+        // next tile (of this item or the next); after the last stage of the
+        // range it is a re-load nobody reads
+        int nkx = ic.kx;
+        if (kk + 1 < seg_n) {
+            ++cst;
+        } else {
+            cst = 0;
+            if (t + 1 == ic.T && ci + 1 < p.count) nkx = sk_item(p, ci + 1).kx;
+        }
+        land(cslot, cst, nkx);
         // MFMAs of steps 6 and 7 with the DMA of a later stage between them,
         // then the next stage's head (at the end of the range these load and
         // read stages nobody uses: the issue cursor stays on the last one)
@@ -471,8 +524,11 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             remaining -= seg_n;
             epilogue(seg_n);
             if (remaining == 0) break;
-            ++t;
-            seg_n = min(remaining, p.ST);
+            if (++t == ic.T) {
+                t = 0;
+                ic = sk_item(p, ++ci);
+            }
+            seg_n = min(remaining, ic.ST);
             kk = 0;
         }
     }
@@ -495,21 +551,24 @@ __global__ __launch_bounds__(kSkReduceThreads) void sk_reduce_kernel(SkParams p)
     const int b = (int)blockIdx.x / kRowBlocks + 1;   // boundary at sk_start(b)
     const int rb = (int)blockIdx.x % kRowBlocks;
     const int s = sk_start(b, p);
-    if (s % p.ST == 0) return;                        // between tiles: no split
-    const int t = s / p.ST;
-    if (sk_start(b - 1, p) > t * p.ST) return;        // an earlier boundary of t does the work
-    const int g_first = b - 1, g_last = sk_owner((t + 1) * p.ST - 1, p);
+    const SkItem it = sk_item(p, sk_find_item(p, s));
+    const int local = s - it.ibeg;
+    if (local % it.ST == 0) return;                   // between tiles: no split
+    const int t = local / it.ST;
+    const int ts = it.ibeg + t * it.ST;               // the tile's first iteration
+    if (sk_start(b - 1, p) > ts) return;              // an earlier boundary of t does the work
+    const int g_first = b - 1, g_last = sk_owner(ts + it.ST - 1, p);
     const int nc = g_last - g_first + 1;              // contributors, at most G <= kSkReduceThreads
     const int tid = (int)threadIdx.x;
     if (tid < nc) {
         const int og = g_first + tid;
-        s_part[tid] = (uint32_t)(og * 2 + (sk_start(og, p) / p.ST == t ? 0 : 1));
+        s_part[tid] = (uint32_t)(og * 2 + (sk_start(og, p) >= ts ? 0 : 1));
     }
     __syncthreads();
     const int c = (tid % kColGroups) * 4;
     const int r0 = rb * kSkReduceRows + tid / kColGroups;
-    const int m0 = (t % p.MT) * kSkBM, n = (t / p.MT) * kSkBN + c;
-    if (n >= p.N) return;
+    const int m0 = (t % it.MT) * kSkBM, n = (t / it.MT) * kSkBN + c;
+    if (n >= it.N) return;
     float4_t sum[kRowsPerThread];
     auto part = [&](int i, int k) __attribute__((always_inline)) {
         return gld((const float4_t *)(p.ws + (size_t)s_part[i] * kSkPartialFloats +
@@ -533,7 +592,7 @@ __global__ __launch_bounds__(kSkReduceThreads) void sk_reduce_kernel(SkParams p)
 #pragma unroll
     for (int k = 0; k < kRowsPerThread; ++k) {
         const int m = m0 + r0 + k * (kSkReduceThreads / kColGroups);
-        if (m < p.M) store_y4(p, m, n, sum[k]);
+        if (m < it.M) store_y4(it, m, n, sum[k]);
     }
 }
 
@@ -586,44 +645,56 @@ int sk_grid(int T, int ST, int cu_count) {
     return (int)best;
 }
 
-hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, hipStream_t stream) {
+SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg) {
     const WeightGeom &g = w->g;
+    SkItem it{};
+    it.q_t = w->q_t;
+    it.s_t = w->s_t;
+    it.zp_t = (const uint8_t *)w->zp_t;
+    it.x = a.x;
+    it.y = a.y;
+    it.ldx = a.ldx;
+    it.kx = a.kx;
+    it.M = a.M;
+    it.N = g.N;
+    it.NT = g.NT;
+    it.ST = g.ST;
+    it.MT = (a.M + kSkBM - 1) / kSkBM;
+    it.T = sk_tiles(a.M, g.NT);
+    it.y_f16 = a.y_type == MNB_F16;
+    it.accumulate = a.accumulate;
+    it.y_vec = (g.N % 4 == 0) && ((uintptr_t)a.y % (it.y_f16 ? 8 : 16) == 0);
+    it.ibeg = ibeg;
+    return it;
+}
+
+// Launches the GEMM over the items (count == 1: `one`, else the device table
+// `items` with host copy `host`) and, when some workgroup range boundary falls
+// inside a tile, the reduce kernel.
+static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem *host, int32_t count, int64_t iters,
+                            int scale_f32, int has_zp, int sps, int G, float *ws, hipStream_t stream) {
+    if (iters >= (int64_t)1 << 31 || G < 1 || G > kSkReduceThreads) return hipErrorInvalidValue;
     SkParams p;
-    p.q_t = (const u32x4_t *)w->q_t;
-    p.s_t = w->s_t;
-    p.zp_t = (const uint8_t *)w->zp_t;
-    p.x = a.x;
-    p.ldx = a.ldx;
-    p.kx = a.kx;
-    p.M = a.M;
-    p.N = g.N;
-    p.NT = g.NT;
-    p.ST = g.ST;
-    p.y = a.y;
-    p.y_f16 = a.y_type == MNB_F16;
-    p.accumulate = a.accumulate;
-    p.y_vec = (g.N % 4 == 0) && ((uintptr_t)a.y % (p.y_f16 ? 8 : 16) == 0);
-    p.MT = (a.M + kSkBM - 1) / kSkBM;
-    p.T = sk_tiles(a.M, g.NT);
+    p.one = one;
+    p.items = items;
+    p.count = count;
     p.G = G;
-    const int64_t iters = (int64_t)p.T * g.ST;
-    if (iters >= (int64_t)1 << 31) return hipErrorInvalidValue;
     p.I = (int32_t)iters;
     p.ws = ws;
     dim3 grid(G), block(kSkThreads);
 #define MNB_SK_LAUNCH(ST_, ZP_, SPS_) hipLaunchKernelGGL((gemm_sk_kernel<ST_, ZP_, SPS_>), grid, block, 0, stream, p)
 #define MNB_SK_SPS(ST_, ZP_)                           \
-    switch (g.SPS) {                                   \
+    switch (sps) {                                     \
         case 1: MNB_SK_LAUNCH(ST_, ZP_, 1); break;     \
         case 2: MNB_SK_LAUNCH(ST_, ZP_, 2); break;     \
         case 4: MNB_SK_LAUNCH(ST_, ZP_, 4); break;     \
         case 8: MNB_SK_LAUNCH(ST_, ZP_, 8); break;     \
         default: return hipErrorInvalidValue;          \
     }
-    if (g.scale_f32) {
-        if (g.has_zp) { MNB_SK_SPS(float, true) } else { MNB_SK_SPS(float, false) }
+    if (scale_f32) {
+        if (has_zp) { MNB_SK_SPS(float, true) } else { MNB_SK_SPS(float, false) }
     } else {
-        if (g.has_zp) { MNB_SK_SPS(_Float16, true) } else { MNB_SK_SPS(_Float16, false) }
+        if (has_zp) { MNB_SK_SPS(_Float16, true) } else { MNB_SK_SPS(_Float16, false) }
     }
 #undef MNB_SK_SPS
 #undef MNB_SK_LAUNCH
@@ -631,12 +702,28 @@ hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float
     if (e != hipSuccess) return e;
     // split tiles exist when some range boundary falls inside a tile
     bool split = false;
-    for (int b = 1; b < G && !split; ++b) split = ((int64_t)b * p.I / G) % g.ST != 0;
+    int32_t k = 0;
+    for (int b = 1; b < G && !split; ++b) {
+        const int64_t s = (int64_t)b * iters / G;
+        while (k + 1 < count && host[k + 1].ibeg <= s) ++k;
+        split = (s - host[k].ibeg) % host[k].ST != 0;
+    }
     if (split) {
         hipLaunchKernelGGL(sk_reduce_kernel, dim3((G - 1) * (kSkBM / kSkReduceRows)), dim3(kSkReduceThreads), 0, stream, p);
         e = hipGetLastError();
     }
     return e;
+}
+
+hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, hipStream_t stream) {
+    const WeightGeom &g = w->g;
+    const SkItem one = sk_make_item(w, a, 0);
+    return launch_sk(one, nullptr, &one, 1, (int64_t)one.T * g.ST, g.scale_f32, g.has_zp, g.SPS, G, ws, stream);
+}
+
+hipError_t launch_gemm_group(const GemmGroupPlan &g, float *ws, hipStream_t stream) {
+    return launch_sk(g.host[0], (const SkItem *)g.items, g.host.data(), g.count, g.iters, g.scale_f32, g.has_zp,
+                     g.sps, g.G, ws, stream);
 }
 
 }  // namespace mnb

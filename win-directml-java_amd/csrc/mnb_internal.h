@@ -32,6 +32,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <vector>
+
 #include "mnb.h"
 
 namespace mnb {
@@ -164,6 +166,31 @@ hipError_t launch_gemv_stream(const GemvGroupPlan &g, hipStream_t stream);
 int stream_kernel_waves_per_cu(int scale_f32, int has_zp, int sps);
 constexpr int kStreamWavesPerBlock = 4;
 
+// One product of a GEMM launch (M > 16): the weight's tiled buffers, x, y and
+// the sizes; ibeg is its first (tile, stage) iteration in the launch.
+struct SkItem {
+    const void *q_t;
+    const void *s_t;
+    const uint8_t *zp_t;
+    const _Float16 *x;
+    void *y;
+    int32_t ldx, kx, M, N;
+    int32_t NT, ST, MT, T;      // n-tiles, super-tiles (stages), m-tiles, output tiles
+    int32_t y_f16, accumulate;
+    int32_t y_vec;              // N % 4 == 0 and y aligned for 4-element stores
+    int32_t ibeg;
+};
+
+// A recorded group of independent products with M > 16 (all items share the
+// kernel variant): one stream-K launch over all their iterations.
+struct GemmGroupPlan {
+    void *items = nullptr;          // device SkItem[count]
+    std::vector<SkItem> host;       // host copy (split detection at launch)
+    int32_t count = 0, G = 0;
+    int64_t iters = 0;
+    int32_t scale_f32 = 0, has_zp = 0, sps = 0;
+};
+
 // Stream-K GEMM (M > 16): G persistent workgroups share the (tile, k-stage)
 // iterations; ws holds sk_workspace_bytes(G) of fp32 partial tiles for the
 // tiles whose stages span workgroups, which a second kernel on the same
@@ -174,6 +201,8 @@ int sk_tiles(int M, int NT);
 // whole tiles per workgroup when that is cheapest, else stream-K).
 int sk_grid(int T, int ST, int cu_count);
 hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, hipStream_t stream);
+SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg);
+hipError_t launch_gemm_group(const GemmGroupPlan &g, float *ws, hipStream_t stream);
 
 // largest M handled by the skinny (GEMV-style) kernel
 constexpr int kSkinnyMaxM = 16;

@@ -374,8 +374,9 @@ class Group:
     """Independent products recorded once and run as one launch (device tensors).
 
     ``entries`` is a list of (Weight, x, y) with torch CUDA tensors; x is fp16
-    [M, K], y fp16 or fp32 [M, N], 1 <= M <= 16.  No item may read another
-    item's output (they may run concurrently)."""
+    [M, K], y fp16 or fp32 [M, N]; all items M == 1, all 1 < M <= 16, or all
+    M > 16.  No item may read another item's output (they may run
+    concurrently)."""
 
     def __init__(self, ctx: Context, entries, accumulate: bool = False):
         L = load()
