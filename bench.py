@@ -14,7 +14,9 @@ M=512, Phi-3-mini shapes"):
   replayed; inputs are resident before the timed region starts.
 * value = algorithmic bytes per step / wall time per step, in GB/s.
 * prefill: the same 129 projections at M = 512 (and a sweep over
-  M = 16, 128, 2048), reported as TFLOP/s (2*M*N*K flops).
+  M = 16, 128, 2048), reported as TFLOP/s (2*M*N*K flops): recorded as one
+  group and run as one launch (like the decode step), and as 129 launches in
+  stream order.
 * roofline: per-launch HIP-event timing of the dominant kernel (the M=1
   kernel) and of the M=512 kernel, against 8 TB/s HBM and 2.5 PFLOP/s fp16.
 * cpu_baseline: the oracle's restatement of the reference's Java CPU path
@@ -60,6 +62,8 @@ def parse():
     p.add_argument("--phase", choices=("all", "decode", "prefill"), default="all",
                    help="decode: only the M=1 group launch and the copy calibration; prefill: only the "
                         "M=512 launches (both for counter runs)")
+    p.add_argument("--prefill-group", action="store_true",
+                   help="with --phase prefill: the 129 projections as one group launch instead of 129 launches")
     return p.parse_args()
 
 
@@ -298,8 +302,12 @@ def main():
     # ---------------- decode step, M = 1 ----------------
     gen = torch.Generator(device="cuda").manual_seed(5)
 
-    # prefill-shaped products: the same 129 projections at M rows, one launch each
-    def prefill(M):
+    # prefill-shaped products: the same 129 projections at M rows, either one
+    # launch each in stream order (group=False; projections of equal N share
+    # one output buffer) or recorded as one group and run as one launch
+    # (group=True; each projection has its own output, as group items may run
+    # concurrently)
+    def prefill(M, group=False):
         xs_m, ys_m = {}, []
         for (_, _, K, N) in projs:
             if K not in xs_m:
@@ -307,27 +315,47 @@ def main():
         xs_l = [xs_m[K] for (_, _, K, _) in projs]
         ybuf = {}
         for (_, _, K, N) in projs:
+            if group:
+                ys_m.append(torch.empty(M, N, device="cuda", dtype=torch.float16))
+                continue
             if N not in ybuf:
                 ybuf[N] = torch.empty(M, N, device="cuda", dtype=torch.float16)
             ys_m.append(ybuf[N])
-        la = Launcher(ctx, weights, xs_l, ys_m, M, stream)
+        if group:
+            la = mnb_hip.Group(ctx, list(zip(weights, xs_l, ys_m)))
+            run = lambda: la.run(stream.cuda_stream)
+        else:
+            la = Launcher(ctx, weights, xs_l, ys_m, M, stream)
+            run = la.run
         if args.eager:
             class _Direct:
                 def replay(self):
-                    la.run()
+                    run()
             g = _Direct()
+        elif group:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(stream):
+                run()           # eager run first
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=stream):
+                run()
+            torch.cuda.synchronize()
         else:
             g = capture(torch, la, stream)
-        steps = max(3, args.steps // 4) if M >= 512 else args.steps
+        steps = max(3, args.steps // 4) if M >= 512 and not group else args.steps
         wall_m, gpu_m = time_graph(torch, g, stream, steps, 2, args.settle_ms)
         flops = sum(2.0 * M * N * K for (_, _, K, N) in projs)
         del g
+        if group:
+            la.close()
+            la = None
         return la, flops, wall_m, gpu_m
 
 
     if args.phase == "prefill":
-        _, fl, w_m, _ = prefill(512)
-        print(json.dumps({"phase": "prefill", "M": 512, "tflops": round(fl / w_m / 1e12, 2),
+        _, fl, w_m, _ = prefill(512, group=args.prefill_group)
+        print(json.dumps({"phase": "prefill", "M": 512, "group": args.prefill_group,
+                          "tflops": round(fl / w_m / 1e12, 2),
                           "us_per_step": round(w_m * 1e6, 1), "flops_per_step": fl}), flush=True)
         for w in weights:
             w.close()
@@ -391,21 +419,34 @@ def main():
     log("per-launch (event brackets): " + json.dumps(per_shape))
 
     # ---------------- prefill, M = 512 (+ sweep) ----------------
-    la512, flops512, wall512, gpu512 = prefill(512)
+    # (1) the 129 projections recorded as one group: one stream-K launch over
+    #     all their tiles (plus the split-tile reduce)
+    _, flops512, wall512, gpu512 = prefill(512, group=True)
     tflops512 = flops512 / wall512 / 1e12
-    # the graph runs the 129 launches back to back (no gaps between kernels),
-    # so the GPU time per replay is the summed kernel time of one step
+    # a replay is the GEMM launch and its reduce back to back, so the GPU time
+    # per replay is the kernel time of one step
     kernel_tflops512 = flops512 / gpu512 / 1e12
-    log("prefill M=512: %.1f us per step, %.1f us GPU time, %.1f TFLOP/s (kernel time %.1f TFLOP/s)" % (
+    log("prefill M=512 as one group launch: %.1f us per step, %.1f us GPU time, %.1f TFLOP/s (kernel time %.1f)" % (
         wall512 * 1e6, gpu512 * 1e6, tflops512, kernel_tflops512))
+    torch.cuda.empty_cache()
+    # (2) the same projections as 129 launches in stream order
+    la512, _, wall512s, gpu512s = prefill(512)
+    tflops512s = flops512 / wall512s / 1e12
+    kernel_tflops512s = flops512 / gpu512s / 1e12
+    log("prefill M=512 as 129 launches: %.1f us per step, %.1f us GPU time, %.1f TFLOP/s (kernel time %.1f)" % (
+        wall512s * 1e6, gpu512s * 1e6, tflops512s, kernel_tflops512s))
     del la512
-    sweep = {}
+    sweep, sweep_seq = {}, {}
     if not args.no_sweep:
         for M in (16, 128, 2048):
-            _, fl, w_m, _ = prefill(M)
+            _, fl, w_m, _ = prefill(M, group=True)
             sweep[str(M)] = round(fl / w_m / 1e12, 2)
-            log("prefill M=%d: %.1f TFLOP/s" % (M, sweep[str(M)]))
             torch.cuda.empty_cache()
+            _, fl, w_m, _ = prefill(M)
+            sweep_seq[str(M)] = round(fl / w_m / 1e12, 2)
+            torch.cuda.empty_cache()
+            log("prefill M=%d: %.1f TFLOP/s as one group launch, %.1f as 129 launches" % (
+                M, sweep[str(M)], sweep_seq[str(M)]))
 
     copy_gbs = copy_bandwidth(torch, stream)
     log("device copy bandwidth: %.0f GB/s" % copy_gbs)
@@ -455,17 +496,34 @@ def main():
                                    "per_shape": per_shape},
         "prefill_m512": {"tflops": round(tflops512, 2), "ms_per_step": round(wall512 * 1e3, 4),
                          "flops_per_step": flops512, "frac_fp16_peak": round(tflops512 / FP16_PEAK_TFLOPS, 4),
+                         "note": "the 129 projections at M=512 (fp16 x and y, each projection with its own "
+                                 "output) recorded as one group and run as one launch, like the decode step",
                          "roofline": {"bound": "mfma", "achieved": round(kernel_tflops512, 2),
                                       "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                       "frac": round(kernel_tflops512 / FP16_PEAK_TFLOPS, 4),
+                                      "kernel": "mnb::gemm_sk_kernel + mnb::sk_reduce_kernel (one group launch per step)",
+                                      "avg_launch_us": round(gpu512 * 1e6, 2),
+                                      "traffic": measured_traffic("gemm_sk_phi3_prefill_m512_group.md",
+                                                                  "traffic_bytes_per_step"),
+                                      "traffic_unit": "HBM bytes per step (one launch)",
+                                      "traffic_source": "profiles/gemm_sk_phi3_prefill_m512_group.md "
+                                                        "(rocprofv3 FETCH_SIZE + WRITE_SIZE)"},
+                         "sweep_tflops": sweep},
+        "prefill_m512_sequential": {
+                         "tflops": round(tflops512s, 2), "ms_per_step": round(wall512s * 1e3, 4),
+                         "frac_fp16_peak": round(tflops512s / FP16_PEAK_TFLOPS, 4),
+                         "note": "the same projections as 129 stream-ordered launches (HIP graph)",
+                         "roofline": {"bound": "mfma", "achieved": round(kernel_tflops512s, 2),
+                                      "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                      "frac": round(kernel_tflops512s / FP16_PEAK_TFLOPS, 4),
                                       "kernel": "mnb::gemm_sk_kernel (M=512, one launch per projection)",
-                                      "avg_launch_us": round(gpu512 / len(projs) * 1e6, 2),
+                                      "avg_launch_us": round(gpu512s / len(projs) * 1e6, 2),
                                       "traffic": measured_traffic("gemm_sk_phi3_prefill_m512.md",
                                                                   "traffic_bytes_per_step"),
                                       "traffic_unit": "HBM bytes per step (129 launches)",
                                       "traffic_source": "profiles/gemm_sk_phi3_prefill_m512.md "
                                                         "(rocprofv3 FETCH_SIZE + WRITE_SIZE)"},
-                         "sweep_tflops": sweep},
+                         "sweep_tflops": sweep_seq},
         "device_copy_gbs": round(copy_gbs, 1),
         "qwen_tied_lm_head": qwen_head,
         "cpu_baseline": cpu,

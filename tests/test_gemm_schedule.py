@@ -1,0 +1,74 @@
+"""Tile-list schedule of a grouped prefill GEMM (mnb::sk_tile_list in
+win-directml-java_amd/csrc/mnb_sched.cpp), checked on the CPU.
+
+The grouped launch replaces a sequence of the reference's batched GEMM
+dispatches (INT4_MATMUL_BATCH_TILED_HLSL, MatMulNBitsKernel.java:732-820,
+one per projection); the reference has no counterpart of this schedule, so
+what is pinned here are its invariants: every output tile of every item is
+computed exactly once, each workgroup's iteration range equals the stages of
+its own tiles (so no tile is split and no partial sums are needed), the
+ranges tile the launch, and the per-workgroup work is balanced."""
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CSRC = os.path.join(ROOT, "win-directml-java_amd", "csrc")
+
+
+@pytest.fixture(scope="module")
+def checker(tmp_path_factory):
+    exe = str(tmp_path_factory.mktemp("sched") / "sched_check")
+    subprocess.run(["g++", "-O2", "-std=c++17", "-Wall", "-Werror", "-I" + CSRC, "-o", exe,
+                    os.path.join(ROOT, "tests", "sched_check.cpp"), os.path.join(CSRC, "mnb_sched.cpp")],
+                   check=True)
+    return exe
+
+
+def run(checker, G, items):
+    """items: (MT, NG, ST) per item.  Returns the checker's figures."""
+    inp = "%d\n" % G + "\n".join("%d %d %d" % t for t in items) + "\n"
+    r = subprocess.run([checker], input=inp, capture_output=True, text=True)
+    assert r.returncode == 0 and r.stdout.startswith("ok"), r.stdout
+    return {k: float(v) for k, v in re.findall(r"(\w+)=([\d.]+)", r.stdout)}
+
+
+def phi3(M):
+    """The Phi-3-mini decode step's 129 projections at M rows: (MT, NG, ST)."""
+    MT = (M + 127) // 128
+    layer = [(3072, 9216), (3072, 3072), (3072, 16384), (8192, 3072)]
+    return [(MT, (N + 255) // 256, (K + 127) // 128) for _ in range(32) for K, N in layer] + \
+        [(MT, (32064 + 255) // 256, 24)]
+
+
+@pytest.mark.parametrize("M", [128, 512, 2048])
+def test_phi3_step_groups(checker, M):
+    f = run(checker, 256, phi3(M))
+    assert f["imbalance"] < (0.06 if M == 128 else 0.01)
+    # side by side on one XCD: a few x row blocks, not one per workgroup
+    assert f["x_blocks"] <= {128: 4, 512: 6, 2048: 16}[M]
+
+
+def test_tile_list_group_of_the_gpu_test(checker):
+    specs = [(512, 3072, 9216), (700, 576, 8000), (2048, 1536, 3072), (300, 8192, 5000), (4500, 256, 1100),
+             (129, 3072, 16384), (64, 200, 30000), (1024, 1024, 4096)]
+    items = [((M + 127) // 128, (N + 255) // 256, (((K + 31) // 32) * 32 + 127) // 128) for M, K, N in specs]
+    f = run(checker, 256, items)
+    assert f["tiles"] == 1142
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_groups(checker, seed):
+    rng = np.random.default_rng(seed)
+    G = int(rng.choice([1, 3, 8, 64, 80, 104, 256]))
+    n = int(rng.integers(1, 40))
+    items = [(int(rng.integers(1, 41)), int(rng.integers(1, 131)), int(rng.integers(1, 71))) for _ in range(n)]
+    run(checker, G, items)
+
+
+def test_more_workgroups_than_tiles(checker):
+    f = run(checker, 256, [(1, 3, 24), (2, 1, 5)])
+    assert f["tiles"] == 5

@@ -477,24 +477,18 @@ def test_group_matches_oracle_and_single_launches(ctx):
         w.close()
 
 
-def test_group_of_prefill_products(ctx):
-    """Independent products with M > 16 recorded as one group: one stream-K
-    launch whose workgroup ranges run across item boundaries (different K, so
-    different stage counts per tile; M and N tails; fp16 and fp32 outputs;
-    y +=).  Every item is within the tolerance of the oracle on sampled rows,
-    within the tolerance of its own single launch, and replays are bitwise
-    identical."""
+def _check_prefill_group(ctx, specs, seed):
+    """Records the products `specs` (M, K, N, y dtype, y +=) as groups (one
+    per accumulate flag) and checks every item against the oracle on sampled
+    rows and against its own single launch, with replays bitwise identical."""
     import torch
-    specs = [(200, 3072, 1000, np.float16, False), (64, 8192, 3072, np.float32, False),
-             (512, 3072, 9216, np.float16, False), (33, 1536, 577, np.float32, True),
-             (300, 576, 1536, np.float16, False)]
     entries, host = [], []
     st = torch.cuda.Stream()
     for i, (M, K, N, ydt, acc) in enumerate(specs):
-        t = synth.make_weight(1200 + i, N, K, 32, with_zp=True)
+        t = synth.make_weight(seed + i, N, K, 32, with_zp=True)
         w = upload(ctx, t)
-        x16 = synth.make_x(1300 + i, M, K)
-        y0 = np.random.default_rng(1400 + i).standard_normal((M, N)).astype(ydt)
+        x16 = synth.make_x(seed + 100 + i, M, K)
+        y0 = np.random.default_rng(seed + 200 + i).standard_normal((M, N)).astype(ydt)
         entries.append((w, torch.from_numpy(x16).cuda(), torch.from_numpy(y0.copy()).cuda()))
         host.append((t, x16, y0, acc))
     torch.cuda.synchronize()
@@ -527,8 +521,52 @@ def test_group_of_prefill_products(ctx):
             err = np.abs(single - y.astype(np.float32))
             assert float(np.max(err - (fp16_ulp(single) if y.dtype == np.float16 else 0.0))) <= tol, label
         g.close()
+    return entries
+
+
+def test_group_of_prefill_products(ctx):
+    """Independent products with M > 16 recorded as one group, few tiles: one
+    stream-K launch whose workgroup ranges run across item boundaries
+    (different K, so different stage counts per tile; M and N tails; fp16 and
+    fp32 outputs; y +=)."""
+    import torch
+    specs = [(200, 3072, 1000, np.float16, False), (64, 8192, 3072, np.float32, False),
+             (512, 3072, 9216, np.float16, False), (33, 1536, 577, np.float32, True),
+             (300, 576, 1536, np.float16, False)]
+    entries = _check_prefill_group(ctx, specs, 1200)
     with pytest.raises(mnb_hip.MnbError):       # M <= 16 and M > 16 do not mix
         mnb_hip.Group(ctx, [entries[0], (entries[1][0], torch.zeros((2, 8192), dtype=torch.float16, device="cuda"),
                                          torch.zeros((2, 3072), dtype=torch.float32, device="cuda"))])
     for w, _, _ in entries:
+        w.close()
+
+
+def test_group_of_prefill_products_in_tile_list_order(ctx):
+    """A group with 1142 output tiles (more than four per workgroup on a
+    256-CU device) runs in tile-list order: whole tiles per workgroup, blocks
+    of tiles that share x rows and weight columns side by side on one XCD.
+    Items cover one to 36 m-tiles, k tails (K = 200, 576), N tails and fp16
+    and fp32 outputs."""
+    specs = [(512, 3072, 9216, np.float16, False), (700, 576, 8000, np.float32, False),
+             (2048, 1536, 3072, np.float16, False), (300, 8192, 5000, np.float16, False),
+             (4500, 256, 1100, np.float32, False), (129, 3072, 16384, np.float16, False),
+             (64, 200, 30000, np.float16, False), (1024, 1024, 4096, np.float32, False)]
+    tiles = sum(((M + 127) // 128) * ((N + 255) // 256) for M, K, N, _, _ in specs)
+    assert tiles == 1142
+    # at 512 columns the group has 589 tiles, fewer than four per workgroup:
+    # it runs with 256-column tiles
+    assert sum(((M + 127) // 128) * ((N + 511) // 512) for M, K, N, _, _ in specs) < 1024
+    for w, _, _ in _check_prefill_group(ctx, specs, 1500):
+        w.close()
+
+
+def test_group_of_prefill_products_with_wide_tiles(ctx):
+    """A group with 1243 tiles of 512 columns runs the 512-column kernel (8
+    waves of 128 x 64) in tile-list order: more than 32 m-tiles (M = 4500),
+    N tails inside a 512-column tile (N = 8000, 30000), k tails (K = 200,
+    576), fp16 and fp32 outputs, zero points."""
+    specs = [(2048, 1536, 16384, np.float16, False), (4500, 256, 8000, np.float32, False),
+             (700, 576, 8000, np.float16, False), (64, 200, 30000, np.float16, False)]
+    assert sum(((M + 127) // 128) * ((N + 511) // 512) for M, K, N, _, _ in specs) == 1243
+    for w, _, _ in _check_prefill_group(ctx, specs, 1700):
         w.close()

@@ -687,17 +687,18 @@ struct mnb_group {
     mnb::GemmGroupPlan gplan;
 };
 
-// A group of products with M > 16: the items' (tile, stage) iterations in
-// group order, one stream-K launch over one workgroup per CU (the iterations
-// of a whole group far exceed the CU count).
+// Whole tiles per workgroup from which a GEMM group runs in tile-list order.
+constexpr int kGemmListTilesPerWg = 4;
+
+// A group of products with M > 16: one launch over one workgroup per CU,
+// the items' (tile, stage) iterations in stream-K order or, for many tiles,
+// in a tile list.
 static int32_t group_create_gemm(mnb_context *ctx, int32_t count, const mnb_group_item *items, mnb_group **out) {
     mnb::GemmGroupPlan plan;
-    plan.host.resize((size_t)count);
-    int64_t iters = 0;
+    std::vector<mnb::MatmulArgs> args((size_t)count);
     for (int32_t i = 0; i < count; ++i) {
         const mnb_group_item &it = items[i];
-        const mnb_weight *w = it.weight;
-        const WeightGeom &g = w->g;
+        const WeightGeom &g = it.weight->g;
         if (i == 0) {
             plan.scale_f32 = g.scale_f32;
             plan.has_zp = g.has_zp;
@@ -707,7 +708,7 @@ static int32_t group_create_gemm(mnb_context *ctx, int32_t count, const mnb_grou
         }
         if ((int64_t)it.M * g.K * 2 >= ((int64_t)1 << 31) || (uint64_t)g.NT * (uint64_t)g.ST * mnb::kTileBytes >= ((uint64_t)1 << 32))
             return fail(MNB_ERR_UNSUPPORTED, "item %d: x of 2 GiB or packed weights of 4 GiB or more in a group", i);
-        mnb::MatmulArgs a;
+        mnb::MatmulArgs &a = args[(size_t)i];
         a.x = (const _Float16 *)it.x;
         a.ldx = g.K;
         a.kx = g.K;
@@ -715,19 +716,52 @@ static int32_t group_create_gemm(mnb_context *ctx, int32_t count, const mnb_grou
         a.y = it.y;
         a.y_type = it.y_type;
         a.accumulate = (it.flags & MNB_ACCUMULATE) ? 1 : 0;
-        plan.host[(size_t)i] = mnb::sk_make_item(w, a, (int32_t)std::min<int64_t>(iters, INT32_MAX));
-        iters += (int64_t)plan.host[(size_t)i].T * g.ST;
-        if (iters >= ((int64_t)1 << 31)) return fail(MNB_ERR_INVALID_ARGUMENT, "group too large");
     }
+    // the items at tile width ntw; false when the launch would have 2^31
+    // iterations or more
+    int64_t tiles = 0;
+    auto build = [&](int ntw) {
+        plan.ntw = ntw;
+        plan.host.resize((size_t)count);
+        plan.iters = 0;
+        tiles = 0;
+        for (int32_t i = 0; i < count; ++i) {
+            plan.host[(size_t)i] = mnb::sk_make_item(items[i].weight, args[(size_t)i], (int32_t)plan.iters, ntw);
+            plan.iters += (int64_t)plan.host[(size_t)i].T * plan.host[(size_t)i].ST;
+            tiles += plan.host[(size_t)i].T;
+            if (plan.iters >= ((int64_t)1 << 31)) return false;
+        }
+        return true;
+    };
+    if (!build(mnb::kGemmNTW)) return fail(MNB_ERR_INVALID_ARGUMENT, "group too large");
     plan.count = count;
-    plan.iters = iters;
-    plan.G = (int32_t)std::min<int64_t>(std::min(ctx->cu_count, 256), iters);
+    plan.G = (int32_t)std::min<int64_t>(std::min(ctx->cu_count, 256), plan.iters);
+    // Tile-list order once every workgroup gets several whole tiles: the
+    // workgroups of one XCD then run tiles that share x rows and weight
+    // columns side by side, and no tile is split, so the 512-column kernel
+    // (half the LDS reads of x per MFMA) can run where the variant has one;
+    // fewer tiles keep the stream-K split, which balances any tile count.
+    std::vector<mnb::SkTile> seq;
+    std::vector<mnb::SkRange> wg;
+    const int64_t min_tiles = (int64_t)kGemmListTilesPerWg * plan.G;
+    if (tiles >= min_tiles) {
+        if (mnb::sk_wide_supported(plan.scale_f32, plan.sps) && (!build(mnb::kGemmWideNTW) || tiles < min_tiles))
+            build(mnb::kGemmNTW);
+        mnb::sk_tile_list(plan.host, plan.G, seq, wg);
+    }
     DeviceGuard guard(ctx->device);
     hipError_t e;
     if ((e = dev_alloc(&plan.items, plan.host.size() * sizeof(mnb::SkItem))) != hipSuccess ||
         (e = hipMemcpy(plan.items, plan.host.data(), plan.host.size() * sizeof(mnb::SkItem), hipMemcpyHostToDevice)) !=
-            hipSuccess) {
+            hipSuccess ||
+        (!seq.empty() &&
+         ((e = dev_alloc(&plan.seq, seq.size() * sizeof(mnb::SkTile))) != hipSuccess ||
+          (e = dev_alloc(&plan.wg, wg.size() * sizeof(mnb::SkRange))) != hipSuccess ||
+          (e = hipMemcpy(plan.seq, seq.data(), seq.size() * sizeof(mnb::SkTile), hipMemcpyHostToDevice)) != hipSuccess ||
+          (e = hipMemcpy(plan.wg, wg.data(), wg.size() * sizeof(mnb::SkRange), hipMemcpyHostToDevice)) != hipSuccess))) {
         if (plan.items) (void)hipFree(plan.items);
+        if (plan.seq) (void)hipFree(plan.seq);
+        if (plan.wg) (void)hipFree(plan.wg);
         return hip_fail(e, "group");
     }
     mnb_group *grp = new mnb_group();
@@ -897,6 +931,8 @@ int32_t mnb_group_destroy(mnb_group *group) {
     DeviceGuard guard(group->ctx->device);
     hipError_t first = hipStreamSynchronize(group->ctx->stream), e;
     if (group->gplan.items && (e = hipFree(group->gplan.items)) != hipSuccess && first == hipSuccess) first = e;
+    if (group->gplan.seq && (e = hipFree(group->gplan.seq)) != hipSuccess && first == hipSuccess) first = e;
+    if (group->gplan.wg && (e = hipFree(group->gplan.wg)) != hipSuccess && first == hipSuccess) first = e;
     if (group->plan.items && (e = hipFree(group->plan.items)) != hipSuccess && first == hipSuccess) first = e;
     if (group->plan.wg_item && (e = hipFree(group->plan.wg_item)) != hipSuccess && first == hipSuccess) first = e;
     if (group->plan.units && (e = hipFree(group->plan.units)) != hipSuccess && first == hipSuccess) first = e;

@@ -44,10 +44,10 @@ namespace mnb {
 
 constexpr int kSkBM = 128;          // rows per tile
 constexpr int kSkWaves = 8;         // two per SIMD
-constexpr int kSkNTW = 2;           // n-tiles (16 rows of W) per wave: 32 columns
+constexpr int kSkNTW = kGemmNTW;    // n-tiles (16 rows of W) per wave: 32 columns
 constexpr int kSkBN = kSkWaves * kSkNTW * kTileRows;   // 256 columns per tile
+constexpr int kSkWideNTW = kGemmWideNTW;   // wide tiles (tile-list launches only): 64 columns per wave, 512 per tile
 constexpr int kSkFM = kSkBM / 32;   // 32-row A fragments per wave
-constexpr int kSkFN = kSkNTW / 2;   // 32-column B fragments per wave
 constexpr int kSkThreads = 64 * kSkWaves;
 constexpr int kSkPartialFloats = kSkBM * kSkBN;   // one fp32 partial tile, [kSkBM][kSkBN] row-major
 constexpr int kSkReduceRows = 16;                 // rows of a partial tile per reduce workgroup
@@ -59,10 +59,19 @@ __device__ __forceinline__ float16_t mfma32x32x16(half8_t a, half8_t b, float16_
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// The launch's parameters: its items and the stream-K split.
+// The launch's parameters: its items and how their iterations are shared.
+// Stream-K order (seq == nullptr): the items' tiles follow one another in
+// group order, tile t of an item covering m-tile t % MT and n-group t / MT,
+// and logical workgroup g owns iterations [g I / G, (g + 1) I / G).
+// Tile-list order (seq != nullptr): the tiles are listed in seq, workgroup
+// after workgroup, and logical workgroup g owns the whole tiles
+// seq[wg[g].pos ..] with iterations [wg[g].iter, wg[g + 1].iter), so no tile
+// is split.
 struct SkParams {
     SkItem one;             // the item when count == 1 (a single product)
     const SkItem *items;    // device table of count items (count > 1), ibeg ascending
+    const SkTile *seq;      // tile-list order: the tiles, workgroup-major (else nullptr)
+    const SkRange *wg;      // tile-list order: G + 1 workgroup starts
     int32_t count;
     int32_t G;              // workgroups
     int32_t I;              // iterations of all items (below 2^31)
@@ -96,8 +105,54 @@ __device__ __forceinline__ int sk_find_item(const SkParams &p, int i) {
     return lo;
 }
 
+// Entry i of the tile list (uniform index, scalar load).
+__device__ __forceinline__ SkTile sk_seq(const SkParams &p, int i) {
+    const __attribute__((address_space(4))) SkTile *s = (const __attribute__((address_space(4))) SkTile *)p.seq;
+    SkTile e;
+    e.item = s[i].item;
+    e.t = s[i].t;
+    return e;
+}
+
+__device__ __forceinline__ SkRange sk_wg(const SkParams &p, int g) {
+    const __attribute__((address_space(4))) SkRange *s = (const __attribute__((address_space(4))) SkRange *)p.wg;
+    SkRange r;
+    r.pos = s[g].pos;
+    r.iter = s[g].iter;
+    return r;
+}
+
 // first iteration of logical workgroup g (g = G gives I)
-__device__ __forceinline__ int sk_start(int g, const SkParams &p) { return (int)((int64_t)g * p.I / p.G); }
+__device__ __forceinline__ int sk_start(int g, const SkParams &p) {
+    if (p.seq) return sk_wg(p, g).iter;
+    return (int)((int64_t)g * p.I / p.G);
+}
+
+// A cursor over the launch's tiles is item ci (fields ic), tile t of that
+// item and, in tile-list order, the list position pos.  Steps it to the next
+// tile of the launch (the caller knows there is one).
+__device__ __forceinline__ void sk_next_tile(const SkParams &p, int &ci, int &t, int &pos, SkItem &ic) {
+    if (p.seq) {
+        const SkTile e = sk_seq(p, ++pos);
+        if (e.item != ci) {
+            ci = e.item;
+            ic = sk_item(p, ci);
+        }
+        t = e.t;
+    } else if (++t == ic.T) {
+        t = 0;
+        ic = sk_item(p, ++ci);
+    }
+}
+
+// k extent of the tile after the cursor's (the caller knows there is one).
+__device__ __forceinline__ int sk_next_kx(const SkParams &p, int ci, int t, int pos, const SkItem &ic) {
+    if (p.seq) {
+        const int item = sk_seq(p, pos + 1).item;
+        return item == ci ? ic.kx : sk_item(p, item).kx;
+    }
+    return t + 1 < ic.T ? ic.kx : sk_item(p, ci + 1).kx;
+}
 
 // logical workgroup owning iteration i
 __device__ __forceinline__ int sk_owner(int i, const SkParams &p) {
@@ -169,10 +224,10 @@ __device__ __forceinline__ void dma16(uint32_t m0, uint32_t off, const void *bas
 }
 
 // Ring slot layout (bytes) for one stage, and the direct loads that fill it.
-template <typename ScaleT, bool HAS_ZP, int SPS>
+template <typename ScaleT, bool HAS_ZP, int SPS, int NTW>
 struct SkSlot {
     static constexpr int ZB = SPS <= 2 ? 1 : SPS / 2;
-    static constexpr int kNT = kSkBN / kTileRows;                   // 16 n-tiles per tile
+    static constexpr int kNT = kSkWaves * NTW;                      // n-tiles per tile (16 or 32)
     static constexpr int kX = 0;                                    // x tile [128][16 chunks]
     static constexpr int kQ = kSkBM * kTileK * 2;                   // 32 KiB: packed tiles [16][64 lanes][16 B]
     static constexpr int kWin = 1024;                               // bytes of one 64-lane direct load
@@ -188,14 +243,16 @@ struct SkSlot {
     // 1 KiB window each of the scale and zero-point regions that contains
     // the wave's own tiles (all 64 lanes load: no lane mask, no branch)
     static constexpr int kXDma = kSkBM * kTileK * 2 / kWin / kSkWaves;
-    static constexpr int kDma = kXDma + kSkNTW + 1 + (HAS_ZP ? 1 : 0);
+    static constexpr int kDma = kXDma + NTW + 1 + (HAS_ZP ? 1 : 0);
     static_assert(kTileS % 16 == 0 && kTileZ % 16 == 0, "16-byte pieces");
-    static_assert(kSkNTW * kTileS <= kWin && kSkNTW * kTileZ <= kWin, "a wave's scales fit one window");
+    static_assert(NTW * kTileS <= kWin && NTW * kTileZ <= kWin, "a wave's scales fit one window");
 };
 
-template <typename ScaleT, bool HAS_ZP, int SPS>
+template <typename ScaleT, bool HAS_ZP, int SPS, int NTW>
 __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
-    using L = SkSlot<ScaleT, HAS_ZP, SPS>;
+    using L = SkSlot<ScaleT, HAS_ZP, SPS, NTW>;
+    constexpr int BN = kSkWaves * NTW * kTileRows;   // columns per tile
+    constexpr int FN = NTW / 2;                      // 32-column weight fragments per wave
     constexpr int ZB = L::ZB;
     constexpr int D = L::kDepth;
     __shared__ __align__(1024) unsigned char ring[D][L::kBytes];
@@ -209,11 +266,24 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     const int g = (p.G % 8 == 0) ? (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8) : (int)blockIdx.x;
     const int i0 = sk_start(g, p), i1 = sk_start(g + 1, p);
     if (i0 >= i1) return;
-    // compute cursor: item ci (fields ic), tile t of the item, stage cst of the tile
-    int ci = sk_find_item(p, i0);
+    // compute cursor: the tile (item fields ic, tile t of the item) and the
+    // stage cst of the tile
+    int ci, t, cpos, cst;
+    if (p.seq) {
+        cpos = sk_wg(p, g).pos;
+        const SkTile e = sk_seq(p, cpos);
+        ci = e.item;
+        t = e.t;
+        cst = 0;
+    } else {
+        cpos = 0;
+        ci = sk_find_item(p, i0);
+    }
     SkItem ic = sk_item(p, ci);
-    int t = (i0 - ic.ibeg) / ic.ST;
-    int cst = (i0 - ic.ibeg) - t * ic.ST;
+    if (!p.seq) {
+        t = (i0 - ic.ibeg) / ic.ST;
+        cst = (i0 - ic.ibeg) - t * ic.ST;
+    }
 
     const uint32_t k6400 = vgpr_const(0x64006400u);
     const uint32_t ring0 = __builtin_amdgcn_readfirstlane(lds_addr(&ring[0][0]));
@@ -231,14 +301,15 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     // workgroup's 16 n-tiles fill the padding.
     constexpr int s_win_max = L::kSRegion - L::kWin;
     constexpr int z_win_max = L::kZRegion - L::kWin;
-    const int s_win = min(wave * kSkNTW * L::kTileS, s_win_max);
-    const int z_win = HAS_ZP ? min(wave * kSkNTW * L::kTileZ, z_win_max) : 0;
-    // issue cursor: item ii (fields iq), tile lt, stage lst, iteration li
-    int ii = ci, lt = t, lst = cst, li = i0, lslot = 0;
+    const int s_win = min(wave * NTW * L::kTileS, s_win_max);
+    const int z_win = HAS_ZP ? min(wave * NTW * L::kTileZ, z_win_max) : 0;
+    // issue cursor: the tile (item fields iq, tile lt of the item), stage lst,
+    // iteration li
+    int ii = ci, lt = t, ipos = cpos, lst = cst, li = i0, lslot = 0;
     SkItem iq = ic;
-    uint32_t xrow[L::kXDma], xcolk[L::kXDma], qoff[kSkNTW], soff = 0, zoff = 0;
+    uint32_t xrow[L::kXDma], xcolk[L::kXDma], qoff[NTW], soff = 0, zoff = 0;
     auto set_tile = [&]() __attribute__((always_inline)) {
-        const int m0 = (lt % iq.MT) * kSkBM, ntg = (lt / iq.MT) * L::kNT, nt0 = ntg + wave * kSkNTW;
+        const int m0 = (lt % iq.MT) * kSkBM, ntg = (lt / iq.MT) * L::kNT, nt0 = ntg + wave * NTW;
 #pragma unroll
         for (int u = 0; u < L::kXDma; ++u) {
             const int row = (wave * L::kXDma + u) * 4 + (lane >> 4);
@@ -246,7 +317,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             xcolk[u] = (uint32_t)(((lane & 15) ^ (row & 15)) * 8);   // k of the chunk this lane loads
         }
 #pragma unroll
-        for (int b = 0; b < kSkNTW; ++b)
+        for (int b = 0; b < NTW; ++b)
             qoff[b] = ((uint32_t)min(nt0 + b, iq.NT - 1) * (uint32_t)iq.ST * 64u + (uint32_t)lane) * 16u;
         {
             const int byte = s_win + lane * 16;
@@ -268,7 +339,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     };
     auto dma_q = [&](uint32_t base, int b) __attribute__((always_inline)) {
         const unsigned char *qb = (const unsigned char *)iq.q_t + (size_t)lst * kTileBytes;
-        dma16(base + L::kQ + (uint32_t)(wave * kSkNTW + b) * kTileBytes, qoff[b], qb);
+        dma16(base + L::kQ + (uint32_t)(wave * NTW + b) * kTileBytes, qoff[b], qb);
     };
     auto dma_sz = [&](uint32_t base) __attribute__((always_inline)) {
         dma16(base + L::kS + (uint32_t)s_win, soff, (const unsigned char *)iq.s_t + (size_t)lst * L::kTileS);
@@ -280,10 +351,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             ++li;
             if (++lst == iq.ST) {
                 lst = 0;
-                if (++lt == iq.T) {
-                    lt = 0;
-                    iq = sk_item(p, ++ii);
-                }
+                sk_next_tile(p, ii, lt, ipos, iq);
                 set_tile();
             }
         }
@@ -294,7 +362,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
 #pragma unroll
         for (int u = 0; u < L::kXDma; ++u) dma_x(base, u);
 #pragma unroll
-        for (int b = 0; b < kSkNTW; ++b) dma_q(base, b);
+        for (int b = 0; b < NTW; ++b) dma_q(base, b);
         dma_sz(base);
         advance();
     };
@@ -302,6 +370,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     // ---- land: wait for the oldest stage in flight, zero its x pieces at
     // k >= kx, and meet the other waves ----
     bool drain = false;   // set after y stores: stores and loads may complete out of order
+    bool first_seg = true;   // the segment being computed is this workgroup's first (partial slot 0)
     auto land = [&](int slot, int st, int kx) __attribute__((always_inline)) {
         if (drain || D == 2) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -322,11 +391,11 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     };
 
-    float16_t acc[kSkFM][kSkFN];
+    float16_t acc[kSkFM][FN];
 #pragma unroll
     for (int a = 0; a < kSkFM; ++a)
 #pragma unroll
-        for (int f = 0; f < kSkFN; ++f)
+        for (int f = 0; f < FN; ++f)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[a][f][v] = 0.f;
 
@@ -335,15 +404,15 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     // tile, column 32 f + 8 (v / 4) + 4 h + v % 4 of the wave's 32 columns.
     auto epilogue = [&](int nst) __attribute__((always_inline)) {
         const int m0 = (t % ic.MT) * kSkBM, ng = t / ic.MT;
-        const int c_wave = wave * kSkNTW * kTileRows;   // first column of this wave in the tile
+        const int c_wave = wave * NTW * kTileRows;   // first column of this wave in the tile
         if (nst == ic.ST) {
-            const int n_wave = ng * kSkBN + c_wave;
+            const int n_wave = ng * BN + c_wave;
 #pragma unroll
             for (int a = 0; a < kSkFM; ++a) {
                 const int m = m0 + a * 32 + c32;
                 if (m < ic.M) {
 #pragma unroll
-                    for (int f = 0; f < kSkFN; ++f)
+                    for (int f = 0; f < FN; ++f)
 #pragma unroll
                         for (int j = 0; j < 4; ++j)
                             store_y4(ic, m, n_wave + f * 32 + 8 * j + 4 * h,
@@ -351,15 +420,16 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
                                                 acc[a][f][4 * j + 3]});
                 }
             }
-        } else {
+        } else if constexpr (NTW == kSkNTW) {
             // partial tile of a split tile: [kSkBM][kSkBN] fp32, summed by sk_reduce_kernel
-            const int slot = i0 >= ic.ibeg + t * ic.ST ? 0 : 1;   // 0 if t is this workgroup's first tile
+            // (wide tiles run in tile-list order only, where no tile is split)
+            const int slot = first_seg ? 0 : 1;
             __attribute__((address_space(1))) float *part =
                 (__attribute__((address_space(1))) float *)p.ws + ((size_t)g * 2 + slot) * kSkPartialFloats;
 #pragma unroll
             for (int a = 0; a < kSkFM; ++a)
 #pragma unroll
-                for (int f = 0; f < kSkFN; ++f)
+                for (int f = 0; f < FN; ++f)
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
                         *(__attribute__((address_space(1))) float4_t *)(part + (a * 32 + c32) * kSkBN + c_wave + f * 32 +
@@ -369,10 +439,11 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
 #pragma unroll
         for (int a = 0; a < kSkFM; ++a)
 #pragma unroll
-            for (int f = 0; f < kSkFN; ++f)
+            for (int f = 0; f < FN; ++f)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[a][f][v] = 0.f;
         drain = true;
+        first_seg = false;
     };
 
     // ---- main loop: segments of one tile, one stage per inner trip ----
@@ -393,14 +464,14 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     // k-group 2 s + h: word s / 2 of tile lane ((2 s + h) % 4) * 16 + c32 % 16.
     // Two 16-byte reads per fragment hold all of them: qb[f][0] for even s,
     // qb[f][1] for odd s.
-    u32x4_t qb[kSkFN][2];
-    ScaleT sc[kSkFN][SPS];
-    uint32_t zb[kSkFN];
+    u32x4_t qb[FN][2];
+    ScaleT sc[FN][SPS];
+    uint32_t zb[FN];
     auto load_stage = [&](int slot) __attribute__((always_inline)) {
         const unsigned char *sl = ring[slot];
 #pragma unroll
-        for (int f = 0; f < kSkFN; ++f) {
-            const int ntl = wave * kSkNTW + 2 * f + (c32 >> 4);
+        for (int f = 0; f < FN; ++f) {
+            const int ntl = wave * NTW + 2 * f + (c32 >> 4);
             const unsigned char *qt = sl + L::kQ + ntl * kTileBytes;
             qb[f][0] = *(const u32x4_t *)(qt + (h * 16 + (c32 & 15)) * 16);
             qb[f][1] = *(const u32x4_t *)(qt + ((2 + h) * 16 + (c32 & 15)) * 16);
@@ -425,10 +496,10 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
         for (int a = 0; a < kSkFM; ++a)
             af[a] = *(const half8_t *)(xs + (a * 32 + c32) * kTileK + (((2 * s + h) ^ (c32 & 15)) * 8));
     };
-    auto dequant = [&](half8_t(&bf)[kSkFN], int s) __attribute__((always_inline)) {
+    auto dequant = [&](half8_t(&bf)[FN], int s) __attribute__((always_inline)) {
         const int si = s * SPS / 8;   // scale block of k-group 2 s + h (same for both h)
 #pragma unroll
-        for (int f = 0; f < kSkFN; ++f) {
+        for (int f = 0; f < FN; ++f) {
             const uint32_t z = HAS_ZP ? zp_nibble(zb[f], si) : 8u;
             half8_t w = unpack_q_minus_zp(qb[f][s & 1][s >> 1], bias_lo_pair(z), bias_hi_pair(z), k6400);
             if constexpr (sizeof(ScaleT) == 2) {
@@ -441,16 +512,16 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             bf[f] = w;
         }
     };
-    auto mfma_step = [&](const half8_t(&af)[kSkFM], const half8_t(&bf)[kSkFN]) __attribute__((always_inline)) {
+    auto mfma_step = [&](const half8_t(&af)[kSkFM], const half8_t(&bf)[FN]) __attribute__((always_inline)) {
 #pragma unroll
         for (int a = 0; a < kSkFM; ++a)
 #pragma unroll
-            for (int f = 0; f < kSkFN; ++f) acc[a][f] = mfma32x32x16(bf[f], af[a], acc[a][f]);
+            for (int f = 0; f < FN; ++f) acc[a][f] = mfma32x32x16(bf[f], af[a], acc[a][f]);
     };
     int cslot = 0;                           // ring slot of the stage being computed
     constexpr int kSteps = kTileK / 16;      // 8 MFMA k-steps per stage
-    half8_t af[2][kSkFM], bf[2][kSkFN];      // steps 0..6, alternating
-    half8_t af7[kSkFM], bf7[kSkFN];          // step 7, held across the barrier
+    half8_t af[2][kSkFM], bf[2][FN];      // steps 0..6, alternating
+    half8_t af7[kSkFM], bf7[FN];          // step 7, held across the barrier
     auto head_reads = [&]() __attribute__((always_inline)) {
         load_stage(cslot);
         read_x(af[0], cslot, 0);
@@ -479,7 +550,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
                 __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // VALU
             }
 #pragma unroll
-            for (int i = 0; i < kSkFM * kSkFN - kSkFM; ++i) {
+            for (int i = 0; i < kSkFM * FN - kSkFM; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
                 __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
             }
@@ -497,7 +568,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             ++cst;
         } else {
             cst = 0;
-            if (t + 1 == ic.T && ci + 1 < p.count) nkx = sk_item(p, ci + 1).kx;
+            if (remaining > seg_n) nkx = sk_next_kx(p, ci, t, cpos, ic);
         }
         land(cslot, cst, nkx);
         // MFMAs of steps 6 and 7 with the DMA of a later stage between them,
@@ -505,16 +576,16 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
         // read stages nobody uses: the issue cursor stays on the last one)
         {
             const uint32_t base = slot_base();
-            static_assert(L::kXDma + kSkNTW < 2 * kSkFM * kSkFN, "one DMA per tail MFMA");
+            static_assert(L::kXDma + NTW < 2 * kSkFM * FN, "one DMA per tail MFMA");
 #pragma unroll
-            for (int i = 0; i < 2 * kSkFM * kSkFN; ++i) {
-                const int a = (i / kSkFN) % kSkFM, f = i % kSkFN;
-                if (i < kSkFM * kSkFN) acc[a][f] = mfma32x32x16(bf[0][f], af[0][a], acc[a][f]);
+            for (int i = 0; i < 2 * kSkFM * FN; ++i) {
+                const int a = (i / FN) % kSkFM, f = i % FN;
+                if (i < kSkFM * FN) acc[a][f] = mfma32x32x16(bf[0][f], af[0][a], acc[a][f]);
                 else acc[a][f] = mfma32x32x16(bf7[f], af7[a], acc[a][f]);
                 __builtin_amdgcn_sched_barrier(0);
                 if (i < L::kXDma) dma_x(base, i);
-                else if (i < L::kXDma + kSkNTW) dma_q(base, i - L::kXDma);
-                else if (i == L::kXDma + kSkNTW) dma_sz(base);
+                else if (i < L::kXDma + NTW) dma_q(base, i - L::kXDma);
+                else if (i == L::kXDma + NTW) dma_sz(base);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -524,10 +595,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             remaining -= seg_n;
             epilogue(seg_n);
             if (remaining == 0) break;
-            if (++t == ic.T) {
-                t = 0;
-                ic = sk_item(p, ++ci);
-            }
+            sk_next_tile(p, ci, t, cpos, ic);
             seg_n = min(remaining, ic.ST);
             kk = 0;
         }
@@ -598,7 +666,15 @@ __global__ __launch_bounds__(kSkReduceThreads) void sk_reduce_kernel(SkParams p)
 
 size_t sk_workspace_bytes(int G) { return (size_t)G * 2 * kSkPartialFloats * sizeof(float); }
 
-int sk_tiles(int M, int NT) { return ((M + kSkBM - 1) / kSkBM) * ((NT * kTileRows + kSkBN - 1) / kSkBN); }
+int sk_tiles(int M, int NT, int ntw) {
+    const int bn = kSkWaves * ntw * kTileRows;
+    return ((M + kSkBM - 1) / kSkBM) * ((NT * kTileRows + bn - 1) / bn);
+}
+
+bool sk_wide_supported(int scale_f32, int sps) {
+    // a wave's scales of its four n-tiles must fit one 1 KiB window
+    return kSkWideNTW * kTileRows * sps * (scale_f32 ? 4 : 2) <= 1024;
+}
 
 // Estimated time of G workgroups (us).  A least-squares fit (4% median error)
 // to 300 timings on MI355X of the Phi-3 projections at M = 128, 512 and 2048
@@ -645,13 +721,13 @@ int sk_grid(int T, int ST, int cu_count) {
     return (int)best;
 }
 
-SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg) {
+SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg, int ntw) {
     const WeightGeom &g = w->g;
     SkItem it{};
     it.q_t = w->q_t;
     it.s_t = w->s_t;
     it.zp_t = (const uint8_t *)w->zp_t;
-    it.x = a.x;
+    it.x = (const void *)a.x;
     it.y = a.y;
     it.ldx = a.ldx;
     it.kx = a.kx;
@@ -660,7 +736,7 @@ SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg) {
     it.NT = g.NT;
     it.ST = g.ST;
     it.MT = (a.M + kSkBM - 1) / kSkBM;
-    it.T = sk_tiles(a.M, g.NT);
+    it.T = sk_tiles(a.M, g.NT, ntw);
     it.y_f16 = a.y_type == MNB_F16;
     it.accumulate = a.accumulate;
     it.y_vec = (g.N % 4 == 0) && ((uintptr_t)a.y % (it.y_f16 ? 8 : 16) == 0);
@@ -668,21 +744,37 @@ SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg) {
     return it;
 }
 
+// The kernel of one weight variant at tile width ntw (wide tiles exist for
+// the variants whose four n-tiles of scales fit one 1 KiB window).
+template <typename ScaleT, bool HAS_ZP, int SPS>
+static void launch_sk_variant(int ntw, dim3 grid, dim3 block, hipStream_t stream, const SkParams &p) {
+    if (ntw == kSkNTW) {
+        hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, kSkNTW>), grid, block, 0, stream, p);
+    } else if constexpr (kSkWideNTW * kTileRows * SPS * sizeof(ScaleT) <= 1024) {
+        hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, kSkWideNTW>), grid, block, 0, stream, p);
+    }
+}
+
 // Launches the GEMM over the items (count == 1: `one`, else the device table
 // `items` with host copy `host`) and, when some workgroup range boundary falls
 // inside a tile, the reduce kernel.
-static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem *host, int32_t count, int64_t iters,
-                            int scale_f32, int has_zp, int sps, int G, float *ws, hipStream_t stream) {
+static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem *host, int32_t count,
+                            const SkTile *seq, const SkRange *wg, int ntw, int64_t iters, int scale_f32, int has_zp,
+                            int sps, int G, float *ws, hipStream_t stream) {
     if (iters >= (int64_t)1 << 31 || G < 1 || G > kSkReduceThreads) return hipErrorInvalidValue;
+    // wide tiles: tile-list order only (no split tiles, no partial tiles)
+    if (ntw != kSkNTW && (ntw != kSkWideNTW || !seq || !sk_wide_supported(scale_f32, sps))) return hipErrorInvalidValue;
     SkParams p;
     p.one = one;
     p.items = items;
+    p.seq = seq;
+    p.wg = wg;
     p.count = count;
     p.G = G;
     p.I = (int32_t)iters;
     p.ws = ws;
     dim3 grid(G), block(kSkThreads);
-#define MNB_SK_LAUNCH(ST_, ZP_, SPS_) hipLaunchKernelGGL((gemm_sk_kernel<ST_, ZP_, SPS_>), grid, block, 0, stream, p)
+#define MNB_SK_LAUNCH(ST_, ZP_, SPS_) launch_sk_variant<ST_, ZP_, SPS_>(ntw, grid, block, stream, p)
 #define MNB_SK_SPS(ST_, ZP_)                           \
     switch (sps) {                                     \
         case 1: MNB_SK_LAUNCH(ST_, ZP_, 1); break;     \
@@ -700,10 +792,11 @@ static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem
 #undef MNB_SK_LAUNCH
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // split tiles exist when some range boundary falls inside a tile
+    // split tiles exist when some range boundary falls inside a tile (never
+    // in tile-list order)
     bool split = false;
     int32_t k = 0;
-    for (int b = 1; b < G && !split; ++b) {
+    for (int b = 1; b < G && !split && !seq; ++b) {
         const int64_t s = (int64_t)b * iters / G;
         while (k + 1 < count && host[k + 1].ibeg <= s) ++k;
         split = (s - host[k].ibeg) % host[k].ST != 0;
@@ -718,12 +811,13 @@ static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem
 hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, hipStream_t stream) {
     const WeightGeom &g = w->g;
     const SkItem one = sk_make_item(w, a, 0);
-    return launch_sk(one, nullptr, &one, 1, (int64_t)one.T * g.ST, g.scale_f32, g.has_zp, g.SPS, G, ws, stream);
+    return launch_sk(one, nullptr, &one, 1, nullptr, nullptr, kSkNTW, (int64_t)one.T * g.ST, g.scale_f32, g.has_zp,
+                     g.SPS, G, ws, stream);
 }
 
 hipError_t launch_gemm_group(const GemmGroupPlan &g, float *ws, hipStream_t stream) {
-    return launch_sk(g.host[0], (const SkItem *)g.items, g.host.data(), g.count, g.iters, g.scale_f32, g.has_zp,
-                     g.sps, g.G, ws, stream);
+    return launch_sk(g.host[0], (const SkItem *)g.items, g.host.data(), g.count, (const SkTile *)g.seq,
+                     (const SkRange *)g.wg, g.ntw, g.iters, g.scale_f32, g.has_zp, g.sps, g.G, ws, stream);
 }
 
 }  // namespace mnb

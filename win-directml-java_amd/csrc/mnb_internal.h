@@ -35,6 +35,7 @@
 #include <vector>
 
 #include "mnb.h"
+#include "mnb_sched.h"
 
 namespace mnb {
 
@@ -166,27 +167,20 @@ hipError_t launch_gemv_stream(const GemvGroupPlan &g, hipStream_t stream);
 int stream_kernel_waves_per_cu(int scale_f32, int has_zp, int sps);
 constexpr int kStreamWavesPerBlock = 4;
 
-// One product of a GEMM launch (M > 16): the weight's tiled buffers, x, y and
-// the sizes; ibeg is its first (tile, stage) iteration in the launch.
-struct SkItem {
-    const void *q_t;
-    const void *s_t;
-    const uint8_t *zp_t;
-    const _Float16 *x;
-    void *y;
-    int32_t ldx, kx, M, N;
-    int32_t NT, ST, MT, T;      // n-tiles, super-tiles (stages), m-tiles, output tiles
-    int32_t y_f16, accumulate;
-    int32_t y_vec;              // N % 4 == 0 and y aligned for 4-element stores
-    int32_t ibeg;
-};
+// n-tiles (16 rows) per wave of the GEMM: 2 (256-column tiles), or 4
+// (512-column tiles, in tile-list order only)
+constexpr int kGemmNTW = 2, kGemmWideNTW = 4;
 
 // A recorded group of independent products with M > 16 (all items share the
-// kernel variant): one stream-K launch over all their iterations.
+// kernel variant): one launch over all their iterations, in stream-K order
+// (seq == nullptr) or in a tile list built at record time.
 struct GemmGroupPlan {
     void *items = nullptr;          // device SkItem[count]
+    void *seq = nullptr;            // device SkTile[tiles] (tile-list order)
+    void *wg = nullptr;             // device SkRange[G + 1] (tile-list order)
     std::vector<SkItem> host;       // host copy (split detection at launch)
     int32_t count = 0, G = 0;
+    int32_t ntw = kGemmNTW;         // n-tiles per wave (kGemmWideNTW: tile-list order only)
     int64_t iters = 0;
     int32_t scale_f32 = 0, has_zp = 0, sps = 0;
 };
@@ -196,12 +190,14 @@ struct GemmGroupPlan {
 // tiles whose stages span workgroups, which a second kernel on the same
 // stream sums in contributor order.
 size_t sk_workspace_bytes(int G);
-int sk_tiles(int M, int NT);
+int sk_tiles(int M, int NT, int ntw = kGemmNTW);
+// whether the weight variant has a 512-column kernel
+bool sk_wide_supported(int scale_f32, int sps);
 // Workgroup count for T tiles of ST stages on cu_count CUs (a cost model:
 // whole tiles per workgroup when that is cheapest, else stream-K).
 int sk_grid(int T, int ST, int cu_count);
 hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, hipStream_t stream);
-SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg);
+SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg, int ntw = kGemmNTW);
 hipError_t launch_gemm_group(const GemmGroupPlan &g, float *ws, hipStream_t stream);
 
 // largest M handled by the skinny (GEMV-style) kernel

@@ -1,0 +1,54 @@
+// mnb_sched.cpp -- host-side work list of a prefill GEMM launch (tile-list
+// order, see mnb_sched.h).
+#include "mnb_sched.h"
+
+#include <algorithm>
+
+namespace mnb {
+
+void sk_tile_list(const std::vector<SkItem> &items, int G, std::vector<SkTile> &seq, std::vector<SkRange> &wg) {
+    constexpr int kBlock = 32;    // tiles of one block: what the workgroups of one XCD run side by side
+    constexpr int kTileCost = 2;  // epilogue of a tile, in stages (balance only)
+    // (1) the launch's tiles in block order
+    std::vector<SkTile> order;
+    for (int i = 0; i < (int)items.size(); ++i) {
+        const SkItem &it = items[(size_t)i];
+        const int MT = it.MT, NG = it.T / it.MT;
+        const int nb = MT <= kBlock ? std::max(1, kBlock / MT) : 1;
+        for (int n0 = 0; n0 < NG; n0 += nb)
+            for (int m = 0; m < MT; ++m)
+                for (int n = n0; n < std::min(NG, n0 + nb); ++n) order.push_back(SkTile{i, m + n * MT});
+    }
+    // (2) one contiguous chunk of equal cost per XCD
+    const int X = G % 8 == 0 ? 8 : 1, per = G / X;
+    int64_t total = 0;
+    for (const SkTile &e : order) total += items[(size_t)e.item].ST + kTileCost;
+    // (3) each chunk dealt to its XCD's workgroups, least loaded first
+    std::vector<std::vector<SkTile>> lists((size_t)G);
+    std::vector<int64_t> load((size_t)G, 0);
+    int64_t before = 0;
+    for (const SkTile &e : order) {
+        const int64_t c = items[(size_t)e.item].ST + kTileCost;
+        const int x = (int)std::min<int64_t>(X - 1, (2 * before + c) * X / (2 * total));
+        before += c;
+        int best = x * per;
+        for (int w = x * per + 1; w < (x + 1) * per; ++w)
+            if (load[(size_t)w] < load[(size_t)best]) best = w;
+        lists[(size_t)best].push_back(e);
+        load[(size_t)best] += c;
+    }
+    // (4) workgroup-major list and the workgroup starts
+    seq.clear();
+    wg.assign((size_t)G + 1, SkRange{0, 0});
+    int64_t iter = 0;
+    for (int g = 0; g < G; ++g) {
+        wg[(size_t)g] = SkRange{(int32_t)seq.size(), (int32_t)iter};
+        for (const SkTile &e : lists[(size_t)g]) {
+            seq.push_back(e);
+            iter += items[(size_t)e.item].ST;
+        }
+    }
+    wg[(size_t)G] = SkRange{(int32_t)seq.size(), (int32_t)iter};
+}
+
+}  // namespace mnb
