@@ -19,6 +19,9 @@ M=512, Phi-3-mini shapes"):
   stream order.
 * roofline: per-launch HIP-event timing of the dominant kernel (the M=1
   kernel) and of the M=512 kernel, against 8 TB/s HBM and 2.5 PFLOP/s fp16.
+* qwen: the Qwen2.5-0.5B tied lm_head (quantized on the device, M=1) and the
+  Qwen step with a quantized lm_head (97 projections, bs 32) as one group
+  launch at M=1 and M=64.
 * cpu_baseline: the oracle's restatement of the reference's Java CPU path
   (8-lane FMA block dot, one thread per core) on a bounded sample of the
   same decode step.
@@ -273,6 +276,58 @@ def qwen_tied_lm_head(torch, mnb_hip, ctx, stream, args):
             "note": "bytes = packed int4 + fp32 scales + zero points + fp16 x and y"}
 
 
+def qwen_step(torch, mnb_hip, ctx, stream, args):
+    """Qwen2.5-0.5B-shaped q4f16 step with a quantized lm_head: 24 layers x
+    {qkv 896->1152, o 896->896, gate_up 896->9728, down 4864->896} + lm_head
+    896->151936, bs 32, fp16 scales in [0.005, 0.02], no zero points.  The 97
+    projections are recorded as one group and replayed in a HIP graph, at
+    M=1 (each with its own activation; GB/s of algorithmic bytes) and at
+    M=64 (one activation per K, one output per projection; TFLOP/s)."""
+    from mnb_hip import synth
+    projs = synth.qwen_decode_step()
+    host, ws = [], []
+    for i, (_, _, K, N) in enumerate(projs):
+        t = synth.make_weight(20_000 + i, N, K, BLOCK)
+        host.append(t)
+        ws.append(mnb_hip.Weight(ctx, N, K, BLOCK, t.q, t.scales_f16))
+    gen = torch.Generator(device="cuda").manual_seed(896)
+    out = {"projections": len(projs), "block_size": BLOCK}
+    for M in (1, 64):
+        if M == 1:
+            xs = [torch.randn(K, device="cuda", generator=gen).half() for (_, _, K, _) in projs]
+        else:
+            xk = {K: torch.randn(M, K, device="cuda", generator=gen).half() for (_, _, K, _) in projs}
+            xs = [xk[K] for (_, _, K, _) in projs]
+        ys = [torch.empty(M, N, device="cuda", dtype=torch.float16) for (_, _, _, N) in projs]
+        grp = mnb_hip.Group(ctx, list(zip(ws, xs, ys)))
+        with torch.cuda.stream(stream):
+            grp.run(stream.cuda_stream)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            grp.run(stream.cuda_stream)
+        wall, gpu = time_graph(torch, g, stream, args.steps, args.warmup, args.settle_ms)
+        del g
+        grp.close()
+        nbytes = sum(t.algorithmic_bytes(M) for t in host)
+        flops = sum(2.0 * M * N * K for (_, _, K, N) in projs)
+        e = {"us_per_step": round(wall * 1e6, 2), "gpu_us_per_step": round(gpu * 1e6, 2), "bytes_per_step": nbytes,
+             "gbs": round(nbytes / wall / 1e9, 1), "tflops": round(flops / wall / 1e12, 2)}
+        if M == 1:
+            e["frac_hbm_peak"] = round(nbytes / wall / 1e9 / HBM_PEAK_GBS, 4)
+            e["kernel"] = "mnb::gemv_stream_kernel (one launch per step)"
+        else:
+            e["frac_fp16_peak"] = round(flops / wall / 1e12 / FP16_PEAK_TFLOPS, 4)
+            e["kernel"] = "mnb::gemm_sk_kernel (one group launch per step)"
+        out["m%d" % M] = e
+        log("qwen step M=%d as one group launch: %.1f us, %.1f GB/s, %.1f TFLOP/s" % (M, wall * 1e6, e["gbs"],
+                                                                                    e["tflops"]))
+        del xs, ys
+    for w in ws:
+        w.close()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -456,6 +511,7 @@ def main():
     del weights
     torch.cuda.empty_cache()
     qwen_head = qwen_tied_lm_head(torch, mnb_hip, ctx, stream, args)
+    qwen = qwen_step(torch, mnb_hip, ctx, stream, args)
     ctx.close()
 
     cpu = None
@@ -526,6 +582,7 @@ def main():
                          "sweep_tflops": sweep_seq},
         "device_copy_gbs": round(copy_gbs, 1),
         "qwen_tied_lm_head": qwen_head,
+        "qwen_step": qwen,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

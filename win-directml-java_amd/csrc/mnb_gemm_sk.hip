@@ -576,6 +576,9 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
         // read stages nobody uses: the issue cursor stays on the last one)
         {
             const uint32_t base = slot_base();
+            // the wave that has passed the barrier issues these first: the
+            // SIMD's other wave is still in its own tail or stage (+0.7%)
+            __builtin_amdgcn_s_setprio(1);
             static_assert(L::kXDma + NTW < 2 * kSkFM * FN, "one DMA per tail MFMA");
 #pragma unroll
             for (int i = 0; i < 2 * kSkFM * FN; ++i) {
@@ -589,6 +592,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+        __builtin_amdgcn_s_setprio(0);
         advance();
         head_reads();
         if (++kk == seg_n) {

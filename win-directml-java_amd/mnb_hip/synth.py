@@ -85,6 +85,17 @@ def zp_row_padded_to_flat(zp_rp: np.ndarray, N: int, kb: int) -> np.ndarray:
     return (flat[0::2] | (flat[1::2] << 4)).astype(np.uint8)
 
 
+def qwen_decode_step() -> List[Tuple[str, int, int, int]]:
+    """(name, layer, K, N) of every quantized projection of one Qwen2.5-0.5B
+    decode step with a quantized lm_head."""
+    out = []
+    for layer in range(QWEN_LAYERS):
+        for name, K, N in QWEN_LAYER:
+            out.append((name, layer, K, N))
+    out.append((QWEN_LM_HEAD[0], QWEN_LAYERS, QWEN_LM_HEAD[1], QWEN_LM_HEAD[2]))
+    return out
+
+
 def phi3_decode_step() -> List[Tuple[str, int, int, int]]:
     """(name, layer, K, N) of every quantized projection of one Phi-3 decode step."""
     out = []
