@@ -67,6 +67,7 @@ def parse():
                         "M=512 launches (both for counter runs)")
     p.add_argument("--prefill-group", action="store_true",
                    help="with --phase prefill: the 129 projections as one group launch instead of 129 launches")
+    p.add_argument("--prefill-m", type=int, default=512, help="with --phase prefill: rows M of the prefill step")
     return p.parse_args()
 
 
@@ -408,8 +409,8 @@ def main():
 
 
     if args.phase == "prefill":
-        _, fl, w_m, _ = prefill(512, group=args.prefill_group)
-        print(json.dumps({"phase": "prefill", "M": 512, "group": args.prefill_group,
+        _, fl, w_m, _ = prefill(args.prefill_m, group=args.prefill_group)
+        print(json.dumps({"phase": "prefill", "M": args.prefill_m, "group": args.prefill_group,
                           "tflops": round(fl / w_m / 1e12, 2),
                           "us_per_step": round(w_m * 1e6, 1), "flops_per_step": fl}), flush=True)
         for w in weights:

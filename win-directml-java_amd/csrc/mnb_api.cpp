@@ -689,6 +689,9 @@ struct mnb_group {
 
 // Whole tiles per workgroup from which a GEMM group runs in tile-list order.
 constexpr int kGemmListTilesPerWg = 4;
+// Cost of a 512-column stage in 256-column stages (same-box A/B of the M=512
+// group: 1046 vs 1155 TFLOP/s, so 2 / 1.105).
+constexpr double kGemmWideStageCost = 1.81;
 
 // A group of products with M > 16: one launch over one workgroup per CU,
 // the items' (tile, stage) iterations in stream-K order or, for many tiles,
@@ -741,13 +744,36 @@ static int32_t group_create_gemm(mnb_context *ctx, int32_t count, const mnb_grou
     // columns side by side, and no tile is split, so the 512-column kernel
     // (half the LDS reads of x per MFMA) can run where the variant has one;
     // fewer tiles keep the stream-K split, which balances any tile count.
+    // The width is the one whose busiest workgroup finishes first: a
+    // 512-column stage has twice the flops of a 256-column one and costs
+    // kGemmWideStageCost of them (a 10.5% gain measured on the M=512 group),
+    // but whole tiles balance worse when they are fewer.
     std::vector<mnb::SkTile> seq;
     std::vector<mnb::SkRange> wg;
     const int64_t min_tiles = (int64_t)kGemmListTilesPerWg * plan.G;
+    auto busiest = [&](const std::vector<mnb::SkRange> &r) {
+        int64_t m = 0;
+        for (int32_t g = 0; g < plan.G; ++g) m = std::max<int64_t>(m, r[(size_t)g + 1].iter - r[(size_t)g].iter);
+        return m;
+    };
     if (tiles >= min_tiles) {
-        if (mnb::sk_wide_supported(plan.scale_f32, plan.sps) && (!build(mnb::kGemmWideNTW) || tiles < min_tiles))
-            build(mnb::kGemmNTW);
         mnb::sk_tile_list(plan.host, plan.G, seq, wg);
+        if (mnb::sk_wide_supported(plan.scale_f32, plan.sps)) {
+            const double narrow = (double)busiest(wg);
+            std::vector<mnb::SkTile> seq_w;
+            std::vector<mnb::SkRange> wg_w;
+            if (build(mnb::kGemmWideNTW) && tiles >= min_tiles) {
+                mnb::sk_tile_list(plan.host, plan.G, seq_w, wg_w);
+                if ((double)busiest(wg_w) * kGemmWideStageCost < narrow) {
+                    seq.swap(seq_w);
+                    wg.swap(wg_w);
+                } else {
+                    build(mnb::kGemmNTW);
+                }
+            } else {
+                build(mnb::kGemmNTW);
+            }
+        }
     }
     DeviceGuard guard(ctx->device);
     hipError_t e;

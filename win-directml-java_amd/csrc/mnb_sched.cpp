@@ -8,16 +8,21 @@ namespace mnb {
 
 void sk_tile_list(const std::vector<SkItem> &items, int G, std::vector<SkTile> &seq, std::vector<SkRange> &wg) {
     constexpr int kBlock = 32;    // tiles of one block: what the workgroups of one XCD run side by side
+    constexpr int kBlockM = 4;    // m-tiles per block (so 8 n-groups): the fewest x and weight bytes per stage
     constexpr int kTileCost = 2;  // epilogue of a tile, in stages (balance only)
-    // (1) the launch's tiles in block order
+    // (1) the launch's tiles in block order: per item, chunks of kBlockM
+    // m-tiles; per chunk, blocks of nb n-groups (consecutive blocks of a
+    // chunk share its x rows)
     std::vector<SkTile> order;
     for (int i = 0; i < (int)items.size(); ++i) {
         const SkItem &it = items[(size_t)i];
         const int MT = it.MT, NG = it.T / it.MT;
-        const int nb = MT <= kBlock ? std::max(1, kBlock / MT) : 1;
-        for (int n0 = 0; n0 < NG; n0 += nb)
-            for (int m = 0; m < MT; ++m)
-                for (int n = n0; n < std::min(NG, n0 + nb); ++n) order.push_back(SkTile{i, m + n * MT});
+        for (int m0 = 0; m0 < MT; m0 += kBlockM) {
+            const int m1 = std::min(MT, m0 + kBlockM), nb = kBlock / (m1 - m0);
+            for (int n0 = 0; n0 < NG; n0 += nb)
+                for (int m = m0; m < m1; ++m)
+                    for (int n = n0; n < std::min(NG, n0 + nb); ++n) order.push_back(SkTile{i, m + n * MT});
+        }
     }
     // (2) one contiguous chunk of equal cost per XCD
     const int X = G % 8 == 0 ? 8 : 1, per = G / X;

@@ -35,8 +35,9 @@ struct SkRange {
 
 // Tile list of a launch over `items` on G workgroups (logical workgroups
 // [x G / 8, (x + 1) G / 8) run on XCD x when G is a multiple of 8): the
-// tiles in blocks that share x rows and weight columns (all m-tiles of up to
-// 32 / MT n-groups), cut into one contiguous chunk of equal stages per XCD,
+// tiles in blocks of 32 that share x rows and weight columns (up to 4
+// m-tiles by 32 / that many n-groups), cut into one contiguous chunk of
+// equal stages per XCD,
 // each chunk dealt tile by tile to the least loaded workgroup of that XCD.
 // Fills seq (workgroup-major, every tile of every item once) and wg (G + 1
 // entries; workgroup g owns seq[wg[g].pos, wg[g + 1].pos), whose stages are
