@@ -407,17 +407,53 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
         const int c_wave = wave * NTW * kTileRows;   // first column of this wave in the tile
         if (nst == ic.ST) {
             const int n_wave = ng * BN + c_wave;
+            // The common case: the wave's 128 x (16 NTW) block lies inside y,
+            // rows are 4-element aligned and y is overwritten.  Then every
+            // lane writes its four rows with one address each and immediate
+            // offsets, without per-group tests.
+            const bool whole = ic.y_vec && !ic.accumulate && m0 + kSkBM <= ic.M && n_wave + NTW * kTileRows <= ic.N;
+            if (whole) {
 #pragma unroll
-            for (int a = 0; a < kSkFM; ++a) {
-                const int m = m0 + a * 32 + c32;
-                if (m < ic.M) {
+                for (int a = 0; a < kSkFM; ++a) {
+                    const size_t row = (size_t)(m0 + a * 32 + c32) * ic.N + n_wave + 4 * h;
+                    if (ic.y_f16) {
+                        __attribute__((address_space(1))) u32x2_t *q =
+                            (__attribute__((address_space(1))) u32x2_t *)((_Float16 *)ic.y + row);
 #pragma unroll
-                    for (int f = 0; f < FN; ++f)
+                        for (int f = 0; f < FN; ++f)
 #pragma unroll
-                        for (int j = 0; j < 4; ++j)
-                            store_y4(ic, m, n_wave + f * 32 + 8 * j + 4 * h,
-                                     (float4_t){acc[a][f][4 * j], acc[a][f][4 * j + 1], acc[a][f][4 * j + 2],
-                                                acc[a][f][4 * j + 3]});
+                            for (int j = 0; j < 4; ++j) {
+                                half2_t h0, h1;
+                                h0[0] = (_Float16)acc[a][f][4 * j];
+                                h0[1] = (_Float16)acc[a][f][4 * j + 1];
+                                h1[0] = (_Float16)acc[a][f][4 * j + 2];
+                                h1[1] = (_Float16)acc[a][f][4 * j + 3];
+                                q[(f * 32 + 8 * j) / 4] = (u32x2_t){as_u32(h0), as_u32(h1)};
+                            }
+                    } else {
+                        __attribute__((address_space(1))) float4_t *q =
+                            (__attribute__((address_space(1))) float4_t *)((float *)ic.y + row);
+#pragma unroll
+                        for (int f = 0; f < FN; ++f)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j)
+                                q[(f * 32 + 8 * j) / 4] = (float4_t){acc[a][f][4 * j], acc[a][f][4 * j + 1],
+                                                                     acc[a][f][4 * j + 2], acc[a][f][4 * j + 3]};
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int a = 0; a < kSkFM; ++a) {
+                    const int m = m0 + a * 32 + c32;
+                    if (m < ic.M) {
+#pragma unroll
+                        for (int f = 0; f < FN; ++f)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j)
+                                store_y4(ic, m, n_wave + f * 32 + 8 * j + 4 * h,
+                                         (float4_t){acc[a][f][4 * j], acc[a][f][4 * j + 1], acc[a][f][4 * j + 2],
+                                                    acc[a][f][4 * j + 3]});
+                    }
                 }
             }
         } else if constexpr (NTW == kSkNTW) {
