@@ -570,3 +570,15 @@ def test_group_of_prefill_products_with_wide_tiles(ctx):
     assert sum(((M + 127) // 128) * ((N + 511) // 512) for M, K, N, _, _ in specs) == 1243
     for w, _, _ in _check_prefill_group(ctx, specs, 1700):
         w.close()
+
+
+def test_group_of_prefill_products_accumulating_in_tile_list_order(ctx):
+    """y += in tile-list order (1412 tiles of 512 columns, enough per
+    workgroup for the wide kernel): the epilogue's general path (read y, add,
+    write) for whole and ragged tiles, N not a multiple of 4, fp16 and fp32
+    outputs, 2, 3 and 5 stages per tile."""
+    specs = [(2000, 384, 16001, np.float32, True), (1500, 256, 30000, np.float16, True),
+             (900, 640, 12000, np.float16, True)]
+    assert sum(((M + 127) // 128) * ((N + 511) // 512) for M, K, N, _, _ in specs) == 1412
+    for w, _, _ in _check_prefill_group(ctx, specs, 1900):
+        w.close()
