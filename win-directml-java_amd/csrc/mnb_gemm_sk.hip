@@ -256,6 +256,11 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     constexpr int ZB = L::ZB;
     constexpr int D = L::kDepth;
     __shared__ __align__(1024) unsigned char ring[D][L::kBytes];
+    // Epilogue staging (wide tiles, where the LDS has room): per wave one
+    // 32 x 32 fp16 block, rows padded to 80 bytes against bank conflicts.
+    constexpr int kStageRow = 80, kStageWave = 32 * kStageRow;
+    constexpr bool kStaged = NTW == kSkWideNTW && D * L::kBytes + kSkWaves * kStageWave <= 160 * 1024;
+    __shared__ __align__(16) unsigned char stage_all[kStaged ? kSkWaves * kStageWave : 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -412,7 +417,38 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             // lane writes its four rows with one address each and immediate
             // offsets, without per-group tests.
             const bool whole = ic.y_vec && !ic.accumulate && m0 + kSkBM <= ic.M && n_wave + NTW * kTileRows <= ic.N;
-            if (whole) {
+            const bool staged = kStaged && whole && ic.y_f16 && ic.N % 8 == 0 && ((uintptr_t)ic.y & 15) == 0;
+            if (staged) {
+                // Per 32 x 32 block: each lane's four 4-column pieces of its
+                // row go to the wave's LDS block, then every lane reads 16
+                // contiguous bytes, so 4 lanes cover a row's 64 bytes and one
+                // store writes 16 rows x 64 bytes (the direct stores write 32
+                // rows x 16 bytes).  The wave's LDS operations run in order,
+                // so the reads see the writes and the next block's writes
+                // follow the reads.
+                unsigned char *sb = stage_all + wave * kStageWave;
+#pragma unroll
+                for (int a = 0; a < kSkFM; ++a)
+#pragma unroll
+                    for (int f = 0; f < FN; ++f) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            half2_t h0, h1;
+                            h0[0] = (_Float16)acc[a][f][4 * j];
+                            h0[1] = (_Float16)acc[a][f][4 * j + 1];
+                            h1[0] = (_Float16)acc[a][f][4 * j + 2];
+                            h1[1] = (_Float16)acc[a][f][4 * j + 3];
+                            *(u32x2_t *)(sb + c32 * kStageRow + (8 * j + 4 * h) * 2) = (u32x2_t){as_u32(h0), as_u32(h1)};
+                        }
+#pragma unroll
+                        for (int k = 0; k < 2; ++k) {
+                            const int r = (lane >> 2) + 16 * k, cc = lane & 3;
+                            const u32x4_t v = *(const u32x4_t *)(sb + r * kStageRow + cc * 16);
+                            *(__attribute__((address_space(1))) u32x4_t *)((_Float16 *)ic.y +
+                                (size_t)(m0 + a * 32 + r) * ic.N + n_wave + f * 32 + cc * 8) = v;
+                        }
+                    }
+            } else if (whole) {
 #pragma unroll
                 for (int a = 0; a < kSkFM; ++a) {
                     const size_t row = (size_t)(m0 + a * 32 + c32) * ic.N + n_wave + 4 * h;
