@@ -477,7 +477,7 @@ def test_group_matches_oracle_and_single_launches(ctx):
         w.close()
 
 
-def _check_prefill_group(ctx, specs, seed):
+def _check_prefill_group(ctx, specs, seed, bs=32):
     """Records the products `specs` (M, K, N, y dtype, y +=) as groups (one
     per accumulate flag) and checks every item against the oracle on sampled
     rows and against its own single launch, with replays bitwise identical."""
@@ -485,7 +485,7 @@ def _check_prefill_group(ctx, specs, seed):
     entries, host = [], []
     st = torch.cuda.Stream()
     for i, (M, K, N, ydt, acc) in enumerate(specs):
-        t = synth.make_weight(seed + i, N, K, 32, with_zp=True)
+        t = synth.make_weight(seed + i, N, K, bs, with_zp=True)
         w = upload(ctx, t)
         x16 = synth.make_x(seed + 100 + i, M, K)
         y0 = np.random.default_rng(seed + 200 + i).standard_normal((M, N)).astype(ydt)
@@ -569,6 +569,16 @@ def test_group_of_prefill_products_with_wide_tiles(ctx):
              (700, 576, 8000, np.float16, False), (64, 200, 30000, np.float16, False)]
     assert sum(((M + 127) // 128) * ((N + 511) // 512) for M, K, N, _, _ in specs) == 1243
     for w, _, _ in _check_prefill_group(ctx, specs, 1700):
+        w.close()
+
+
+@pytest.mark.parametrize("bs", [64, 128])
+def test_group_with_wide_tiles_other_block_sizes(ctx, bs):
+    """The 512-column kernel for 2 and 1 scales per 128-k stage (bs 64 and
+    128, with zero points): 2096 tiles, whole and ragged."""
+    specs = [(4500, 256, 16000, np.float16, False), (2048, 256, 30000, np.float16, False)]
+    assert sum(((M + 127) // 128) * ((N + 511) // 512) for M, K, N, _, _ in specs) == 2096
+    for w, _, _ in _check_prefill_group(ctx, specs, 2100 + bs, bs):
         w.close()
 
 

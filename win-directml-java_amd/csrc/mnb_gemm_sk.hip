@@ -54,6 +54,11 @@ constexpr int kSkReduceRows = 16;                 // rows of a partial tile per 
 constexpr int kSkReduceThreads = 256;             // each thread: 4 rows x 4 columns
 
 typedef float float16_t __attribute__((ext_vector_type(16)));
+// LDS staging of the epilogue is written in 8-byte and read in 16-byte
+// pieces: both types may alias anything, so the compiler keeps every store
+// and never moves a read above the stores it depends on.
+typedef uint32_t u32x2_alias_t __attribute__((ext_vector_type(2), may_alias));
+typedef uint32_t u32x4_alias_t __attribute__((ext_vector_type(4), may_alias));
 
 __device__ __forceinline__ float16_t mfma32x32x16(half8_t a, half8_t b, float16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -438,15 +443,18 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
                             h0[1] = (_Float16)acc[a][f][4 * j + 1];
                             h1[0] = (_Float16)acc[a][f][4 * j + 2];
                             h1[1] = (_Float16)acc[a][f][4 * j + 3];
-                            *(u32x2_t *)(sb + c32 * kStageRow + (8 * j + 4 * h) * 2) = (u32x2_t){as_u32(h0), as_u32(h1)};
+                            *(u32x2_alias_t *)(sb + c32 * kStageRow + (8 * j + 4 * h) * 2) =
+                                (u32x2_alias_t){as_u32(h0), as_u32(h1)};
                         }
+                        asm volatile("" ::: "memory");   // the reads below follow the writes
 #pragma unroll
                         for (int k = 0; k < 2; ++k) {
                             const int r = (lane >> 2) + 16 * k, cc = lane & 3;
-                            const u32x4_t v = *(const u32x4_t *)(sb + r * kStageRow + cc * 16);
+                            const u32x4_alias_t v = *(const u32x4_alias_t *)(sb + r * kStageRow + cc * 16);
                             *(__attribute__((address_space(1))) u32x4_t *)((_Float16 *)ic.y +
-                                (size_t)(m0 + a * 32 + r) * ic.N + n_wave + f * 32 + cc * 8) = v;
+                                (size_t)(m0 + a * 32 + r) * ic.N + n_wave + f * 32 + cc * 8) = (u32x4_t)v;
                         }
+                        asm volatile("" ::: "memory");   // the next block's writes follow these reads
                     }
             } else if (whole) {
 #pragma unroll
