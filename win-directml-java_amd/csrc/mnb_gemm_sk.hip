@@ -8,7 +8,8 @@
 // Output tile 128 (M) x 256 (N) per workgroup of 8 waves (two per SIMD, so
 // one wave's LDS and dequant latency hides behind the other's MFMAs), each
 // wave 128 x 32: four 32-row x fragments against one 32-column weight
-// fragment of v_mfma_f32_32x32x16_f16, fp32 accumulators.  The weight
+// fragment of v_mfma_f32_32x32x16_f16, fp32 accumulators (512-column tiles:
+// two weight fragments per wave, see the work split below).  The weight
 // fragment is the MFMA's A operand and x its B operand, so the accumulators
 // hold y transposed: each lane owns four consecutive columns of one row per
 // 4-register group and writes them with one 8-byte (fp16) or 16-byte (fp32)
@@ -17,25 +18,33 @@
 // the x tile (32 KiB), the packed weight tiles (16 KiB), their scales and zero
 // points -- is copied straight from HBM into a 3-slot LDS ring by direct
 // global->LDS loads while stage s computes, so no load ever passes through
-// registers and two stages of latency are hidden.  Per 16-k step a wave
+// registers and two stages of latency are hidden (a 2-slot ring, one stage,
+// where three slots do not fit the 160 KiB LDS).  Per 16-k step a wave
 // dequantizes its weight fragment in registers (w = (q - zp) * scale, scale
 // folded into the fp16 operand) and runs 4 MFMAs against four x fragments.
 // x rows are stored with chunk c of row m at slot c ^ (m & 15), so the
 // fragment reads are free of bank conflicts.
 //
-// Stream-K: the grid is one persistent workgroup per CU.  The (tile, stage)
-// iterations of the whole launch are cut into equal contiguous ranges, one
-// per workgroup, so every CU gets the same MFMA work whatever the tile count.
-// A launch covers one product (mnb_matmul) or a recorded group of
-// independent products (mnb_group_*, M > 16): the items' iterations follow
-// one another, and a workgroup's range may run from one item into the next.
-// A workgroup that owns all stages of a tile writes y directly.  A tile whose
-// stages span several workgroups is written as fp32 partial tiles, one per
-// contributor, and summed in contributor order by sk_reduce_kernel, launched
-// right after on the same stream over the whole chip; no workgroup ever
-// waits for another.  Logical workgroup ids are laid out XCD-contiguous, so
-// neighbouring workgroups (which share tiles and weight columns) sit on the
-// same XCD.
+// Work split: the grid is one persistent workgroup per CU.  A launch covers
+// one product (mnb_matmul) or a recorded group of independent products
+// (mnb_group_*, M > 16), in one of two orders:
+// - Stream-K: the (tile, stage) iterations of the launch (the items' tiles
+//   one after another) are cut into equal contiguous ranges, one per
+//   workgroup, so every CU gets the same MFMA work whatever the tile count; a
+//   range may run from one item into the next.  A workgroup that owns all
+//   stages of a tile writes y directly.  A tile whose stages span several
+//   workgroups is written as fp32 partial tiles, one per contributor, and
+//   summed in contributor order by sk_reduce_kernel, launched right after on
+//   the same stream over the whole chip; no workgroup ever waits for another.
+// - Tile list (groups with several tiles per workgroup): a host-built list
+//   (mnb_sched.cpp) gives each workgroup whole tiles, ordered so that the
+//   workgroups of one XCD run tiles sharing x rows and weight columns side by
+//   side; no tile is split.  These launches may use 512-column tiles (8 waves
+//   of 128 x 64, a two-slot ring), which halve the LDS reads of x per MFMA,
+//   and stage whole fp16 output tiles through LDS so that each store writes
+//   16 rows x 64 bytes.
+// Logical workgroup ids are laid out XCD-contiguous, so neighbouring
+// workgroups (which share tiles and weight columns) sit on the same XCD.
 #include <algorithm>
 
 #include "mnb_device.h"
