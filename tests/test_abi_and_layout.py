@@ -36,6 +36,28 @@ def test_library_exports_every_declared_symbol():
     assert mnb_hip.load().mnb_version() == 1
 
 
+def test_struct_layouts_match_the_header(tmp_path):
+    """The C structs a foreign binding lays out by hand (the ctypes binding
+    here; the Java FFM binding's 72-byte mnb_group_item) have the header's
+    size and field offsets."""
+    import ctypes
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "mnb.h"\n'
+                   'int main(void) { printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\\n", sizeof(mnb_group_item),\n'
+                   '  offsetof(mnb_group_item, weight), offsetof(mnb_group_item, M), offsetof(mnb_group_item, x),\n'
+                   '  offsetof(mnb_group_item, x_type), offsetof(mnb_group_item, x_elems), offsetof(mnb_group_item, y),\n'
+                   '  offsetof(mnb_group_item, y_type), offsetof(mnb_group_item, y_elems), offsetof(mnb_group_item, flags));\n'
+                   '  return 0; }\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I" + os.path.dirname(HEADER), "-o", str(exe), str(src)], check=True)
+    c = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    G = mnb_hip.GroupItem
+    py = [ctypes.sizeof(G)] + [getattr(G, f).offset for f in
+                               ("weight", "M", "x", "x_type", "x_elems", "y", "y_type", "y_elems", "flags")]
+    assert c == py
+    assert c == [72, 0, 8, 16, 24, 32, 40, 48, 56, 64]   # the offsets the Java binding writes
+
+
 def test_no_device_or_device_path_reports_status():
     import ctypes
     L = mnb_hip.load()
