@@ -582,6 +582,23 @@ def test_group_with_wide_tiles_other_block_sizes(ctx, bs):
         w.close()
 
 
+@pytest.mark.parametrize("seed", [0, 1])
+def test_random_prefill_groups(ctx, seed):
+    """Random groups of prefill products (17 <= M <= 2000, K a multiple of 8
+    up to 1024, 1 <= N <= 24000, random output type) with at least 1100
+    256-column tiles, so they run in tile-list order, with 256- or 512-column
+    tiles as the schedule chooses."""
+    rng = np.random.default_rng(4200 + seed)
+    specs, tiles = [], 0
+    ydt = [np.float16, np.float32][int(rng.integers(0, 2))]
+    while tiles < 1100:
+        M, K, N = int(rng.integers(17, 2001)), 8 * int(rng.integers(1, 129)), int(rng.integers(1, 24001))
+        specs.append((M, K, N, ydt, False))
+        tiles += ((M + 127) // 128) * ((N + 255) // 256)
+    for w, _, _ in _check_prefill_group(ctx, specs, 4300 + 100 * seed):
+        w.close()
+
+
 def test_group_of_prefill_products_accumulating_in_tile_list_order(ctx):
     """y += in tile-list order (1412 tiles of 512 columns, enough per
     workgroup for the wide kernel): the epilogue's general path (read y, add,
