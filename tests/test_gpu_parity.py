@@ -599,6 +599,29 @@ def test_random_prefill_groups(ctx, seed):
         w.close()
 
 
+def test_group_of_skinny_products_as_weight_stream(ctx):
+    """A large group with 1 < M <= 16 (1115 tiles of 32 x 512) runs on the
+    GEMM kernel with 32-row tiles in tile-list order: M of 2, 7, 9 and 16
+    (rows past M clamped and dropped), k tails (K = 200, 1000), N tails, fp16
+    and fp32 outputs.  Each single launch runs the GEMV kernel, so the two
+    paths check each other besides the oracle."""
+    specs = [(16, 256, 200000, np.float16, False), (7, 200, 150001, np.float32, False),
+             (2, 64, 100000, np.float16, False), (9, 1000, 120000, np.float16, False)]
+    assert sum((N + 511) // 512 for M, K, N, _, _ in specs) == 1115
+    for w, _, _ in _check_prefill_group(ctx, specs, 2300):
+        w.close()
+
+
+def test_group_of_short_products_with_32_row_tiles(ctx):
+    """16 < M <= 32 in a large group (1173 tiles): 32-row tiles, with M = 32
+    filling a whole tile (the staged epilogue) and M = 17, 24 ragged."""
+    specs = [(32, 512, 150000, np.float16, False), (17, 256, 200000, np.float32, False),
+             (24, 128, 250000, np.float16, False)]
+    assert sum((N + 511) // 512 for M, K, N, _, _ in specs) == 1173
+    for w, _, _ in _check_prefill_group(ctx, specs, 2400):
+        w.close()
+
+
 def test_group_of_prefill_products_accumulating_in_tile_list_order(ctx):
     """y += in tile-list order (1412 tiles of 512 columns, enough per
     workgroup for the wide kernel): the epilogue's general path (read y, add,

@@ -689,6 +689,8 @@ struct mnb_group {
 
 // Whole tiles per workgroup from which a GEMM group runs in tile-list order.
 constexpr int kGemmListTilesPerWg = 4;
+// Largest M of a group's items for 32-row tiles.
+constexpr int kGemmSkinnyMaxM = 32;
 // Cost of a 512-column stage in 256-column stages (same-box A/B of the M=512
 // group: 1046 vs 1155 TFLOP/s, so 2 / 1.105).
 constexpr double kGemmWideStageCost = 1.81;
@@ -723,13 +725,14 @@ static int32_t group_create_gemm(mnb_context *ctx, int32_t count, const mnb_grou
     // the items at tile width ntw; false when the launch would have 2^31
     // iterations or more
     int64_t tiles = 0;
-    auto build = [&](int ntw) {
+    auto build = [&](int ntw, int fm = mnb::kGemmFM) {
         plan.ntw = ntw;
+        plan.fm = fm;
         plan.host.resize((size_t)count);
         plan.iters = 0;
         tiles = 0;
         for (int32_t i = 0; i < count; ++i) {
-            plan.host[(size_t)i] = mnb::sk_make_item(items[i].weight, args[(size_t)i], (int32_t)plan.iters, ntw);
+            plan.host[(size_t)i] = mnb::sk_make_item(items[i].weight, args[(size_t)i], (int32_t)plan.iters, ntw, fm);
             plan.iters += (int64_t)plan.host[(size_t)i].T * plan.host[(size_t)i].ST;
             tiles += plan.host[(size_t)i].T;
             if (plan.iters >= ((int64_t)1 << 31)) return false;
@@ -756,7 +759,16 @@ static int32_t group_create_gemm(mnb_context *ctx, int32_t count, const mnb_grou
         for (int32_t g = 0; g < plan.G; ++g) m = std::max<int64_t>(m, r[(size_t)g + 1].iter - r[(size_t)g].iter);
         return m;
     };
-    if (tiles >= min_tiles) {
+    // Rows of at most 32 per item: 32-row tiles of 512 columns (a weight
+    // stream; 128-row tiles would multiply by up to 8 the MFMA work).
+    int32_t max_m = 0;
+    for (int32_t i = 0; i < count; ++i) max_m = std::max(max_m, items[i].M);
+    if (max_m <= kGemmSkinnyMaxM && mnb::sk_wide_supported(plan.scale_f32, plan.sps) &&
+        build(mnb::kGemmWideNTW, mnb::kGemmSkinnyFM) && tiles >= min_tiles) {
+        mnb::sk_tile_list(plan.host, plan.G, seq, wg);
+    } else if (!build(mnb::kGemmNTW)) {
+        return fail(MNB_ERR_INVALID_ARGUMENT, "group too large");
+    } else if (tiles >= min_tiles) {
         mnb::sk_tile_list(plan.host, plan.G, seq, wg);
         if (mnb::sk_wide_supported(plan.scale_f32, plan.sps)) {
             const double narrow = (double)busiest(wg);
@@ -854,6 +866,16 @@ int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *
         if (waves > plan.waves) plan.waves = waves;
     }
     if (items[0].M > mnb::kSkinnyMaxM) return group_create_gemm(ctx, count, items, out);
+    // 1 < M <= 16 with many 32 x 512 tiles: the GEMM's weight stream (x
+    // shared by the workgroup's waves in LDS, persistent workgroups) beats one
+    // workgroup per n-tile, whose waves each read their own x rows.
+    if (!plan.m1 && mnb::sk_wide_supported(plan.scale_f32, plan.sps)) {
+        int64_t skinny_tiles = 0;
+        for (int32_t i = 0; i < count; ++i)
+            skinny_tiles += mnb::sk_tiles(items[i].M, items[i].weight->g.NT, mnb::kGemmWideNTW, mnb::kGemmSkinnyFM);
+        if (skinny_tiles >= (int64_t)kGemmListTilesPerWg * std::min(ctx->cu_count, 256))
+            return group_create_gemm(ctx, count, items, out);
+    }
     if (wgs > std::numeric_limits<int32_t>::max()) return fail(MNB_ERR_INVALID_ARGUMENT, "group too large");
     std::vector<uint16_t> wg_item((size_t)wgs);
     for (int32_t i = 0; i < count; ++i) {

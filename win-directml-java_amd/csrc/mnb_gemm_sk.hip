@@ -57,6 +57,7 @@ constexpr int kSkNTW = kGemmNTW;    // n-tiles (16 rows of W) per wave: 32 colum
 constexpr int kSkBN = kSkWaves * kSkNTW * kTileRows;   // 256 columns per tile
 constexpr int kSkWideNTW = kGemmWideNTW;   // wide tiles (tile-list launches only): 64 columns per wave, 512 per tile
 constexpr int kSkFM = kSkBM / 32;   // 32-row A fragments per wave
+constexpr int kSkSkinnyFM = kGemmSkinnyFM;   // skinny tiles (tile-list launches only): 32 rows
 constexpr int kSkThreads = 64 * kSkWaves;
 constexpr int kSkPartialFloats = kSkBM * kSkBN;   // one fp32 partial tile, [kSkBM][kSkBN] row-major
 constexpr int kSkReduceRows = 16;                 // rows of a partial tile per reduce workgroup
@@ -238,12 +239,13 @@ __device__ __forceinline__ void dma16(uint32_t m0, uint32_t off, const void *bas
 }
 
 // Ring slot layout (bytes) for one stage, and the direct loads that fill it.
-template <typename ScaleT, bool HAS_ZP, int SPS, int NTW>
+template <typename ScaleT, bool HAS_ZP, int SPS, int NTW, int FM>
 struct SkSlot {
+    static constexpr int BM = 32 * FM;                              // rows per tile
     static constexpr int ZB = SPS <= 2 ? 1 : SPS / 2;
     static constexpr int kNT = kSkWaves * NTW;                      // n-tiles per tile (16 or 32)
     static constexpr int kX = 0;                                    // x tile [128][16 chunks]
-    static constexpr int kQ = kSkBM * kTileK * 2;                   // 32 KiB: packed tiles [16][64 lanes][16 B]
+    static constexpr int kQ = BM * kTileK * 2;                      // packed tiles [16][64 lanes][16 B] after the x tile
     static constexpr int kWin = 1024;                               // bytes of one 64-lane direct load
     static constexpr int kS = kQ + kNT * kTileBytes;                // scales [16 tiles][16 rows][SPS]
     static constexpr int kTileS = kTileRows * SPS * (int)sizeof(ScaleT);   // scale bytes per tile
@@ -256,15 +258,16 @@ struct SkSlot {
     // per wave and stage: x pieces of 4 rows, its packed tiles, and one
     // 1 KiB window each of the scale and zero-point regions that contains
     // the wave's own tiles (all 64 lanes load: no lane mask, no branch)
-    static constexpr int kXDma = kSkBM * kTileK * 2 / kWin / kSkWaves;
+    static constexpr int kXDma = BM * kTileK * 2 / kWin / kSkWaves;
     static constexpr int kDma = kXDma + NTW + 1 + (HAS_ZP ? 1 : 0);
     static_assert(kTileS % 16 == 0 && kTileZ % 16 == 0, "16-byte pieces");
     static_assert(NTW * kTileS <= kWin && NTW * kTileZ <= kWin, "a wave's scales fit one window");
 };
 
-template <typename ScaleT, bool HAS_ZP, int SPS, int NTW>
+template <typename ScaleT, bool HAS_ZP, int SPS, int NTW, int FM>
 __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
-    using L = SkSlot<ScaleT, HAS_ZP, SPS, NTW>;
+    using L = SkSlot<ScaleT, HAS_ZP, SPS, NTW, FM>;
+    constexpr int BM = L::BM;                        // rows per tile (128, or 32 for skinny tiles)
     constexpr int BN = kSkWaves * NTW * kTileRows;   // columns per tile
     constexpr int FN = NTW / 2;                      // 32-column weight fragments per wave
     constexpr int ZB = L::ZB;
@@ -328,7 +331,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     SkItem iq = ic;
     uint32_t xrow[L::kXDma], xcolk[L::kXDma], qoff[NTW], soff = 0, zoff = 0;
     auto set_tile = [&]() __attribute__((always_inline)) {
-        const int m0 = (lt % iq.MT) * kSkBM, ntg = (lt / iq.MT) * L::kNT, nt0 = ntg + wave * NTW;
+        const int m0 = (lt % iq.MT) * BM, ntg = (lt / iq.MT) * L::kNT, nt0 = ntg + wave * NTW;
 #pragma unroll
         for (int u = 0; u < L::kXDma; ++u) {
             const int row = (wave * L::kXDma + u) * 4 + (lane >> 4);
@@ -410,9 +413,9 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     };
 
-    float16_t acc[kSkFM][FN];
+    float16_t acc[FM][FN];
 #pragma unroll
-    for (int a = 0; a < kSkFM; ++a)
+    for (int a = 0; a < FM; ++a)
 #pragma unroll
         for (int f = 0; f < FN; ++f)
 #pragma unroll
@@ -422,7 +425,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     // Fragment (a, f), register v of lane (c32, h): row a * 32 + c32 of the
     // tile, column 32 f + 8 (v / 4) + 4 h + v % 4 of the wave's 32 columns.
     auto epilogue = [&](int nst) __attribute__((always_inline)) {
-        const int m0 = (t % ic.MT) * kSkBM, ng = t / ic.MT;
+        const int m0 = (t % ic.MT) * BM, ng = t / ic.MT;
         const int c_wave = wave * NTW * kTileRows;   // first column of this wave in the tile
         if (nst == ic.ST) {
             const int n_wave = ng * BN + c_wave;
@@ -430,7 +433,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             // rows are 4-element aligned and y is overwritten.  Then every
             // lane writes its four rows with one address each and immediate
             // offsets, without per-group tests.
-            const bool whole = ic.y_vec && !ic.accumulate && m0 + kSkBM <= ic.M && n_wave + NTW * kTileRows <= ic.N;
+            const bool whole = ic.y_vec && !ic.accumulate && m0 + BM <= ic.M && n_wave + NTW * kTileRows <= ic.N;
             const bool staged = kStaged && whole && ic.y_f16 && ic.N % 8 == 0 && ((uintptr_t)ic.y & 15) == 0;
             if (staged) {
                 // Per 32 x 32 block: each lane's four 4-column pieces of its
@@ -442,7 +445,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
                 // follow the reads.
                 unsigned char *sb = stage_all + wave * kStageWave;
 #pragma unroll
-                for (int a = 0; a < kSkFM; ++a)
+                for (int a = 0; a < FM; ++a)
 #pragma unroll
                     for (int f = 0; f < FN; ++f) {
 #pragma unroll
@@ -467,7 +470,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
                     }
             } else if (whole) {
 #pragma unroll
-                for (int a = 0; a < kSkFM; ++a) {
+                for (int a = 0; a < FM; ++a) {
                     const size_t row = (size_t)(m0 + a * 32 + c32) * ic.N + n_wave + 4 * h;
                     if (ic.y_f16) {
                         __attribute__((address_space(1))) u32x2_t *q =
@@ -496,7 +499,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
                 }
             } else {
 #pragma unroll
-                for (int a = 0; a < kSkFM; ++a) {
+                for (int a = 0; a < FM; ++a) {
                     const int m = m0 + a * 32 + c32;
                     if (m < ic.M) {
 #pragma unroll
@@ -509,14 +512,14 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
                     }
                 }
             }
-        } else if constexpr (NTW == kSkNTW) {
-            // partial tile of a split tile: [kSkBM][kSkBN] fp32, summed by sk_reduce_kernel
-            // (wide tiles run in tile-list order only, where no tile is split)
+        } else if constexpr (NTW == kSkNTW && FM == kSkFM) {
+            // partial tile of a split tile: [BM][kSkBN] fp32, summed by sk_reduce_kernel
+            // (wide and skinny tiles run in tile-list order only, where no tile is split)
             const int slot = first_seg ? 0 : 1;
             __attribute__((address_space(1))) float *part =
                 (__attribute__((address_space(1))) float *)p.ws + ((size_t)g * 2 + slot) * kSkPartialFloats;
 #pragma unroll
-            for (int a = 0; a < kSkFM; ++a)
+            for (int a = 0; a < FM; ++a)
 #pragma unroll
                 for (int f = 0; f < FN; ++f)
 #pragma unroll
@@ -526,7 +529,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
                             (float4_t){acc[a][f][4 * j], acc[a][f][4 * j + 1], acc[a][f][4 * j + 2], acc[a][f][4 * j + 3]};
         }
 #pragma unroll
-        for (int a = 0; a < kSkFM; ++a)
+        for (int a = 0; a < FM; ++a)
 #pragma unroll
             for (int f = 0; f < FN; ++f)
 #pragma unroll
@@ -578,11 +581,11 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             }
         }
     };
-    auto read_x = [&](half8_t(&af)[kSkFM], int slot, int s) __attribute__((always_inline)) {
+    auto read_x = [&](half8_t(&af)[FM], int slot, int s) __attribute__((always_inline)) {
         // row a * 32 + c32 (row & 15 == c32 & 15), k-chunk 2 s + h
         const _Float16 *xs = (const _Float16 *)(ring[slot] + L::kX);
 #pragma unroll
-        for (int a = 0; a < kSkFM; ++a)
+        for (int a = 0; a < FM; ++a)
             af[a] = *(const half8_t *)(xs + (a * 32 + c32) * kTileK + (((2 * s + h) ^ (c32 & 15)) * 8));
     };
     auto dequant = [&](half8_t(&bf)[FN], int s) __attribute__((always_inline)) {
@@ -601,16 +604,16 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             bf[f] = w;
         }
     };
-    auto mfma_step = [&](const half8_t(&af)[kSkFM], const half8_t(&bf)[FN]) __attribute__((always_inline)) {
+    auto mfma_step = [&](const half8_t(&af)[FM], const half8_t(&bf)[FN]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int a = 0; a < kSkFM; ++a)
+        for (int a = 0; a < FM; ++a)
 #pragma unroll
             for (int f = 0; f < FN; ++f) acc[a][f] = mfma32x32x16(bf[f], af[a], acc[a][f]);
     };
     int cslot = 0;                           // ring slot of the stage being computed
     constexpr int kSteps = kTileK / 16;      // 8 MFMA k-steps per stage
-    half8_t af[2][kSkFM], bf[2][FN];      // steps 0..6, alternating
-    half8_t af7[kSkFM], bf7[FN];          // step 7, held across the barrier
+    half8_t af[2][FM], bf[2][FN];      // steps 0..6, alternating
+    half8_t af7[FM], bf7[FN];          // step 7, held across the barrier
     auto head_reads = [&]() __attribute__((always_inline)) {
         load_stage(cslot);
         read_x(af[0], cslot, 0);
@@ -633,13 +636,13 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             // order within the step: the next step's x reads go out first,
             // between the MFMAs, and its dequant VALU fills the MFMA shadow
 #pragma unroll
-            for (int i = 0; i < kSkFM; ++i) {
+            for (int i = 0; i < FM; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
                 __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // VALU
             }
 #pragma unroll
-            for (int i = 0; i < kSkFM * FN - kSkFM; ++i) {
+            for (int i = 0; i < FM * FN - FM; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
                 __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
             }
@@ -668,12 +671,14 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             // the wave that has passed the barrier issues these first: the
             // SIMD's other wave is still in its own tail or stage (+0.7%)
             __builtin_amdgcn_s_setprio(1);
-            static_assert(L::kXDma + NTW < 2 * kSkFM * FN, "one DMA per tail MFMA");
+            // one DMA after each tail MFMA (skinny tiles: the DMA left over
+            // after the last MFMA follows it)
+            constexpr int kTailMfma = 2 * FM * FN, kTailDma = L::kXDma + NTW + 1;
 #pragma unroll
-            for (int i = 0; i < 2 * kSkFM * FN; ++i) {
-                const int a = (i / FN) % kSkFM, f = i % FN;
-                if (i < kSkFM * FN) acc[a][f] = mfma32x32x16(bf[0][f], af[0][a], acc[a][f]);
-                else acc[a][f] = mfma32x32x16(bf7[f], af7[a], acc[a][f]);
+            for (int i = 0; i < (kTailMfma > kTailDma ? kTailMfma : kTailDma); ++i) {
+                const int a = (i / FN) % FM, f = i % FN;
+                if (i < FM * FN) acc[a][f] = mfma32x32x16(bf[0][f], af[0][a], acc[a][f]);
+                else if (i < kTailMfma) acc[a][f] = mfma32x32x16(bf7[f], af7[a], acc[a][f]);
                 __builtin_amdgcn_sched_barrier(0);
                 if (i < L::kXDma) dma_x(base, i);
                 else if (i < L::kXDma + NTW) dma_q(base, i - L::kXDma);
@@ -759,9 +764,9 @@ __global__ __launch_bounds__(kSkReduceThreads) void sk_reduce_kernel(SkParams p)
 
 size_t sk_workspace_bytes(int G) { return (size_t)G * 2 * kSkPartialFloats * sizeof(float); }
 
-int sk_tiles(int M, int NT, int ntw) {
-    const int bn = kSkWaves * ntw * kTileRows;
-    return ((M + kSkBM - 1) / kSkBM) * ((NT * kTileRows + bn - 1) / bn);
+int sk_tiles(int M, int NT, int ntw, int fm) {
+    const int bn = kSkWaves * ntw * kTileRows, bm = 32 * fm;
+    return ((M + bm - 1) / bm) * ((NT * kTileRows + bn - 1) / bn);
 }
 
 bool sk_wide_supported(int scale_f32, int sps) {
@@ -814,7 +819,7 @@ int sk_grid(int T, int ST, int cu_count) {
     return (int)best;
 }
 
-SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg, int ntw) {
+SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg, int ntw, int fm) {
     const WeightGeom &g = w->g;
     SkItem it{};
     it.q_t = w->q_t;
@@ -828,8 +833,8 @@ SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg, int 
     it.N = g.N;
     it.NT = g.NT;
     it.ST = g.ST;
-    it.MT = (a.M + kSkBM - 1) / kSkBM;
-    it.T = sk_tiles(a.M, g.NT, ntw);
+    it.MT = (a.M + 32 * fm - 1) / (32 * fm);
+    it.T = sk_tiles(a.M, g.NT, ntw, fm);
     it.y_f16 = a.y_type == MNB_F16;
     it.accumulate = a.accumulate;
     it.y_vec = (g.N % 4 == 0) && ((uintptr_t)a.y % (it.y_f16 ? 8 : 16) == 0);
@@ -837,14 +842,18 @@ SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg, int 
     return it;
 }
 
-// The kernel of one weight variant at tile width ntw (wide tiles exist for
-// the variants whose four n-tiles of scales fit one 1 KiB window).
+// The kernel of one weight variant at tile width ntw and height 32 fm (wide
+// and skinny tiles exist for the variants whose four n-tiles of scales fit
+// one 1 KiB window).
 template <typename ScaleT, bool HAS_ZP, int SPS>
-static void launch_sk_variant(int ntw, dim3 grid, dim3 block, hipStream_t stream, const SkParams &p) {
+static void launch_sk_variant(int ntw, int fm, dim3 grid, dim3 block, hipStream_t stream, const SkParams &p) {
     if (ntw == kSkNTW) {
-        hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, kSkNTW>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, kSkNTW, kSkFM>), grid, block, 0, stream, p);
     } else if constexpr (kSkWideNTW * kTileRows * SPS * sizeof(ScaleT) <= 1024) {
-        hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, kSkWideNTW>), grid, block, 0, stream, p);
+        if (fm == kSkFM)
+            hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, kSkWideNTW, kSkFM>), grid, block, 0, stream, p);
+        else
+            hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, kSkWideNTW, kSkSkinnyFM>), grid, block, 0, stream, p);
     }
 }
 
@@ -852,11 +861,14 @@ static void launch_sk_variant(int ntw, dim3 grid, dim3 block, hipStream_t stream
 // `items` with host copy `host`) and, when some workgroup range boundary falls
 // inside a tile, the reduce kernel.
 static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem *host, int32_t count,
-                            const SkTile *seq, const SkRange *wg, int ntw, int64_t iters, int scale_f32, int has_zp,
-                            int sps, int G, float *ws, hipStream_t stream) {
+                            const SkTile *seq, const SkRange *wg, int ntw, int fm, int64_t iters, int scale_f32,
+                            int has_zp, int sps, int G, float *ws, hipStream_t stream) {
     if (iters >= (int64_t)1 << 31 || G < 1 || G > kSkReduceThreads) return hipErrorInvalidValue;
-    // wide tiles: tile-list order only (no split tiles, no partial tiles)
-    if (ntw != kSkNTW && (ntw != kSkWideNTW || !seq || !sk_wide_supported(scale_f32, sps))) return hipErrorInvalidValue;
+    // 256 x 128 tiles, or wide (512 x 128) and skinny (512 x 32) tiles in
+    // tile-list order only (no split tiles, no partial tiles)
+    const bool narrow = ntw == kSkNTW && fm == kSkFM;
+    const bool wide = ntw == kSkWideNTW && (fm == kSkFM || fm == kSkSkinnyFM);
+    if (!narrow && (!wide || !seq || !sk_wide_supported(scale_f32, sps))) return hipErrorInvalidValue;
     SkParams p;
     p.one = one;
     p.items = items;
@@ -867,7 +879,7 @@ static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem
     p.I = (int32_t)iters;
     p.ws = ws;
     dim3 grid(G), block(kSkThreads);
-#define MNB_SK_LAUNCH(ST_, ZP_, SPS_) launch_sk_variant<ST_, ZP_, SPS_>(ntw, grid, block, stream, p)
+#define MNB_SK_LAUNCH(ST_, ZP_, SPS_) launch_sk_variant<ST_, ZP_, SPS_>(ntw, fm, grid, block, stream, p)
 #define MNB_SK_SPS(ST_, ZP_)                           \
     switch (sps) {                                     \
         case 1: MNB_SK_LAUNCH(ST_, ZP_, 1); break;     \
@@ -904,13 +916,13 @@ static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem
 hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, hipStream_t stream) {
     const WeightGeom &g = w->g;
     const SkItem one = sk_make_item(w, a, 0);
-    return launch_sk(one, nullptr, &one, 1, nullptr, nullptr, kSkNTW, (int64_t)one.T * g.ST, g.scale_f32, g.has_zp,
-                     g.SPS, G, ws, stream);
+    return launch_sk(one, nullptr, &one, 1, nullptr, nullptr, kSkNTW, kSkFM, (int64_t)one.T * g.ST, g.scale_f32,
+                     g.has_zp, g.SPS, G, ws, stream);
 }
 
 hipError_t launch_gemm_group(const GemmGroupPlan &g, float *ws, hipStream_t stream) {
     return launch_sk(g.host[0], (const SkItem *)g.items, g.host.data(), g.count, (const SkTile *)g.seq,
-                     (const SkRange *)g.wg, g.ntw, g.iters, g.scale_f32, g.has_zp, g.sps, g.G, ws, stream);
+                     (const SkRange *)g.wg, g.ntw, g.fm, g.iters, g.scale_f32, g.has_zp, g.sps, g.G, ws, stream);
 }
 
 }  // namespace mnb

@@ -168,8 +168,11 @@ int stream_kernel_waves_per_cu(int scale_f32, int has_zp, int sps);
 constexpr int kStreamWavesPerBlock = 4;
 
 // n-tiles (16 rows) per wave of the GEMM: 2 (256-column tiles), or 4
-// (512-column tiles, in tile-list order only)
+// (512-column tiles, in tile-list order only); 32-row fragments per tile: 4
+// (128 rows), or 1 (32-row skinny tiles, with 512 columns, in tile-list
+// order only)
 constexpr int kGemmNTW = 2, kGemmWideNTW = 4;
+constexpr int kGemmFM = 4, kGemmSkinnyFM = 1;
 
 // A recorded group of independent products with M > 16 (all items share the
 // kernel variant): one launch over all their iterations, in stream-K order
@@ -181,6 +184,7 @@ struct GemmGroupPlan {
     std::vector<SkItem> host;       // host copy (split detection at launch)
     int32_t count = 0, G = 0;
     int32_t ntw = kGemmNTW;         // n-tiles per wave (kGemmWideNTW: tile-list order only)
+    int32_t fm = kGemmFM;           // 32-row fragments per tile (kGemmSkinnyFM: tile-list order, wide)
     int64_t iters = 0;
     int32_t scale_f32 = 0, has_zp = 0, sps = 0;
 };
@@ -190,14 +194,14 @@ struct GemmGroupPlan {
 // tiles whose stages span workgroups, which a second kernel on the same
 // stream sums in contributor order.
 size_t sk_workspace_bytes(int G);
-int sk_tiles(int M, int NT, int ntw = kGemmNTW);
+int sk_tiles(int M, int NT, int ntw = kGemmNTW, int fm = kGemmFM);
 // whether the weight variant has a 512-column kernel
 bool sk_wide_supported(int scale_f32, int sps);
 // Workgroup count for T tiles of ST stages on cu_count CUs (a cost model:
 // whole tiles per workgroup when that is cheapest, else stream-K).
 int sk_grid(int T, int ST, int cu_count);
 hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, hipStream_t stream);
-SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg, int ntw = kGemmNTW);
+SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg, int ntw = kGemmNTW, int fm = kGemmFM);
 hipError_t launch_gemm_group(const GemmGroupPlan &g, float *ws, hipStream_t stream);
 
 // largest M handled by the skinny (GEMV-style) kernel
