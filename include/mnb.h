@@ -215,9 +215,11 @@ int32_t mnb_max_batch_rows(void);
  * aligned), y [M, N] fp16 or fp32, M >= 1; all items share the weight variant
  * (scale type, zero points or not, block size class) and one M class: all
  * M == 1 (one persistent streaming launch), all 1 < M <= 16, or all M > 16
- * (prefill-shaped products: one stream-K GEMM launch over all items'
- * tiles, plus its split-tile reduce, using the context's GEMM workspace, so
- * it must not overlap other M > 16 calls on the context).  The group keeps
+ * (prefill-shaped products: one GEMM launch over all items' tiles).  A GEMM
+ * group with few tiles splits tiles across workgroups (stream-K) and then
+ * uses the context's GEMM workspace, so it must not overlap other M > 16
+ * calls on the context; a group with many tiles (also one of 1 < M <= 16)
+ * gives each workgroup whole tiles and uses no workspace.  The group keeps
  * its own device descriptor table, so mnb_group_run allocates nothing and can
  * be captured in a HIP graph. */
 typedef struct mnb_group mnb_group;

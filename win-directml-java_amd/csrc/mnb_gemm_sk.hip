@@ -42,7 +42,9 @@
 //   side; no tile is split.  These launches may use 512-column tiles (8 waves
 //   of 128 x 64, a two-slot ring), which halve the LDS reads of x per MFMA,
 //   and stage whole fp16 output tiles through LDS so that each store writes
-//   16 rows x 64 bytes.
+//   16 rows x 64 bytes; and, for groups whose M is at most 32 (down to
+//   M = 2), 32 x 512 tiles (one 32-row fragment per wave, a three-slot ring):
+//   then the kernel is a weight stream whose x rows are shared in LDS.
 // Logical workgroup ids are laid out XCD-contiguous, so neighbouring
 // workgroups (which share tiles and weight columns) sit on the same XCD.
 #include <algorithm>
