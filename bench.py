@@ -62,9 +62,9 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-sweep", action="store_true")
     p.add_argument("--eager", action="store_true", help="launch directly instead of via HIP graphs (counter runs)")
-    p.add_argument("--phase", choices=("all", "decode", "prefill"), default="all",
+    p.add_argument("--phase", choices=("all", "decode", "prefill", "qwen"), default="all",
                    help="decode: only the M=1 group launch and the copy calibration; prefill: only the "
-                        "M=512 launches (both for counter runs)")
+                        "M=512 launches (both for counter runs); qwen: only the Qwen2.5-0.5B step at M=1 and 64")
     p.add_argument("--prefill-group", action="store_true",
                    help="with --phase prefill: the 129 projections as one group launch instead of 129 launches")
     p.add_argument("--prefill-m", type=int, default=512, help="with --phase prefill: rows M of the prefill step")
@@ -343,6 +343,10 @@ def main():
     info = ctx.info()
     log("device %s %s, %d CUs" % (info.name.decode(), info.arch.decode(), info.compute_units))
     stream = torch.cuda.Stream()
+    if args.phase == "qwen":
+        print(json.dumps({"phase": "qwen", "qwen_step": qwen_step(torch, mnb_hip, ctx, stream, args)}), flush=True)
+        ctx.close()
+        return
 
     projs = synth.phi3_decode_step()
     host, weights = [], []

@@ -28,19 +28,33 @@ void sk_tile_list(const std::vector<SkItem> &items, int G, std::vector<SkTile> &
     const int X = G % 8 == 0 ? 8 : 1, per = G / X;
     int64_t total = 0;
     for (const SkTile &e : order) total += items[(size_t)e.item].ST + kTileCost;
-    // (3) each chunk dealt to its XCD's workgroups, least loaded first
-    std::vector<std::vector<SkTile>> lists((size_t)G);
-    std::vector<int64_t> load((size_t)G, 0);
+    // (3) each chunk dealt to its XCD's workgroups, least loaded first, its
+    // longest tiles first (a stable order, so each item's tiles keep their
+    // block order and still run side by side; longest first keeps the
+    // busiest workgroup close to the mean when tile lengths differ)
+    std::vector<std::vector<SkTile>> chunks((size_t)X);
     int64_t before = 0;
     for (const SkTile &e : order) {
         const int64_t c = items[(size_t)e.item].ST + kTileCost;
         const int x = (int)std::min<int64_t>(X - 1, (2 * before + c) * X / (2 * total));
         before += c;
-        int best = x * per;
-        for (int w = x * per + 1; w < (x + 1) * per; ++w)
-            if (load[(size_t)w] < load[(size_t)best]) best = w;
-        lists[(size_t)best].push_back(e);
-        load[(size_t)best] += c;
+        chunks[(size_t)x].push_back(e);
+    }
+    std::vector<std::vector<SkTile>> lists((size_t)G);
+    std::vector<int64_t> load((size_t)G, 0);
+    for (int x = 0; x < X; ++x) {
+        std::vector<SkTile> &ch = chunks[(size_t)x];
+        std::stable_sort(ch.begin(), ch.end(), [&](const SkTile &a, const SkTile &b) {
+            return items[(size_t)a.item].ST > items[(size_t)b.item].ST;
+        });
+        for (const SkTile &e : ch) {
+            const int64_t c = items[(size_t)e.item].ST + kTileCost;
+            int best = x * per;
+            for (int w = x * per + 1; w < (x + 1) * per; ++w)
+                if (load[(size_t)w] < load[(size_t)best]) best = w;
+            lists[(size_t)best].push_back(e);
+            load[(size_t)best] += c;
+        }
     }
     // (4) workgroup-major list and the workgroup starts
     seq.clear();

@@ -38,7 +38,8 @@ struct SkRange {
 // tiles in blocks of 32 that share x rows and weight columns (up to 4
 // m-tiles by 32 / that many n-groups), cut into one contiguous chunk of
 // equal stages per XCD,
-// each chunk dealt tile by tile to the least loaded workgroup of that XCD.
+// each chunk dealt tile by tile, longest tiles first (stable), to the least
+// loaded workgroup of that XCD.
 // Fills seq (workgroup-major, every tile of every item once) and wg (G + 1
 // entries; workgroup g owns seq[wg[g].pos, wg[g + 1].pos), whose stages are
 // the iterations [wg[g].iter, wg[g + 1].iter)).
