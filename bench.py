@@ -19,6 +19,8 @@ M=512, Phi-3-mini shapes"):
   stream order.
 * roofline: per-launch HIP-event timing of the dominant kernel (the M=1
   kernel) and of the M=512 kernel, against 8 TB/s HBM and 2.5 PFLOP/s fp16.
+* config0: the single qkv product (M=1) as back-to-back launches over 17
+  weight copies (each launch reads from HBM).
 * qwen: the Qwen2.5-0.5B tied lm_head (quantized on the device, M=1) and the
   Qwen step with a quantized lm_head (97 projections, bs 32) as one group
   launch at M=1 and M=64.
@@ -277,6 +279,36 @@ def qwen_tied_lm_head(torch, mnb_hip, ctx, stream, args):
             "note": "bytes = packed int4 + fp32 scales + zero points + fp16 x and y"}
 
 
+def config0_qkv(torch, mnb_hip, ctx, stream, args):
+    """The single MatMulNBits op of the reference's CPU case: M=1, K=3072,
+    N=9216 (Phi-3-mini fused qkv), bs 32, fp16 scales, no zero points, fp16
+    x and y.  17 device copies of the weight (272 MB, more than the 256 MB
+    MALL) are used in turn by 68 back-to-back launches captured in a HIP
+    graph, so each launch reads its weight from HBM; the per-launch time is
+    the graph's GPU time / 68."""
+    from mnb_hip import synth
+    N, K, copies, per_replay = 9216, 3072, 17, 68
+    t = synth.make_weight(0, N, K, BLOCK)
+    ws = [mnb_hip.Weight(ctx, N, K, BLOCK, t.q, t.scales_f16) for _ in range(copies)]
+    gen = torch.Generator(device="cuda").manual_seed(3072)
+    x = torch.randn(K, device="cuda", generator=gen).half()
+    y = torch.empty(N, device="cuda", dtype=torch.float16)
+    la = Launcher(ctx, [ws[i % copies] for i in range(per_replay)], [x] * per_replay, [y] * per_replay, 1, stream)
+    g = capture(torch, la, stream)
+    wall, gpu = time_graph(torch, g, stream, args.steps, args.warmup, args.settle_ms)
+    del g
+    for w in ws:
+        w.close()
+    us = gpu / per_replay * 1e6
+    nbytes = t.algorithmic_bytes(1)
+    gbs = nbytes / us / 1e3
+    log("config 0 (qkv 3072->9216, M=1, single launches from HBM): %.2f us, %.1f GB/s" % (us, gbs))
+    return {"shape": [N, K], "block_size": BLOCK, "avg_launch_us": round(us, 3), "bytes_per_launch": nbytes,
+            "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "kernel": "mnb::gemv_kernel (one launch per product)",
+            "timing": "GPU time of graph replays of 68 back-to-back launches over 17 weight copies (272 MB) / 68"}
+
+
 def qwen_step(torch, mnb_hip, ctx, stream, args):
     """Qwen2.5-0.5B-shaped q4f16 step with a quantized lm_head: 24 layers x
     {qkv 896->1152, o 896->896, gate_up 896->9728, down 4864->896} + lm_head
@@ -515,6 +547,7 @@ def main():
         w.close()
     del weights
     torch.cuda.empty_cache()
+    cfg0 = config0_qkv(torch, mnb_hip, ctx, stream, args)
     qwen_head = qwen_tied_lm_head(torch, mnb_hip, ctx, stream, args)
     qwen = qwen_step(torch, mnb_hip, ctx, stream, args)
     ctx.close()
@@ -586,6 +619,7 @@ def main():
                                                         "(rocprofv3 FETCH_SIZE + WRITE_SIZE)"},
                          "sweep_tflops": sweep_seq},
         "device_copy_gbs": round(copy_gbs, 1),
+        "config0_single_qkv": cfg0,
         "qwen_tied_lm_head": qwen_head,
         "qwen_step": qwen,
         "cpu_baseline": cpu,
