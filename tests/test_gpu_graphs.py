@@ -91,3 +91,70 @@ def test_graph_capture_replays_match_eager():
     finally:
         torch.cuda.synchronize()
         ctx.close()
+
+
+def test_graph_capture_of_tile_list_groups():
+    """Group launches in tile-list order (a prefill group with 512-column
+    tiles and a 1 < M <= 16 group on 32-row tiles) captured into one HIP
+    graph; every replay, with new activations written between replays,
+    equals the eager launches bit for bit."""
+    import torch
+    ctx = mnb_hip.Context(0)
+    try:
+        dev = "cuda"
+        gen = torch.Generator(device=dev).manual_seed(11)
+        groups, xs, ys, ws = [], [], [], []
+        # 1344 tiles of 128 x 512 and 1075 tiles of 32 x 512: both run in tile-list order
+        for gi, (M, shapes) in enumerate([(512, [(3072, 16384), (3072, 9216), (8192, 3072)] * 6),
+                                           (8, [(256, 200000), (512, 200000), (128, 150000)])]):
+            items = []
+            for i, (K, N) in enumerate(shapes):
+                w = _weight(ctx, 100 * gi + i, N, K)
+                x = torch.empty(M, K, device=dev, dtype=torch.float16)
+                y = torch.empty(M, N, device=dev, dtype=torch.float16)
+                ws.append(w)
+                xs.append(x)
+                ys.append(y)
+                items.append((w, x, y))
+            groups.append(mnb_hip.Group(ctx, items))
+        st = torch.cuda.Stream()
+
+        def fill():
+            for x in xs:
+                x.copy_(torch.randn(x.shape, device=dev, generator=gen).half())
+
+        def record():
+            for g in groups:
+                g.run(st.cuda_stream)
+
+        with torch.cuda.stream(st):
+            fill()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=st):
+            record()
+        torch.cuda.synchronize()
+        for rep in range(3):
+            with torch.cuda.stream(st):
+                fill()
+                for y in ys:
+                    y.fill_(float("nan"))
+                graph.replay()
+            torch.cuda.synchronize()
+            got = [y.clone() for y in ys]
+            with torch.cuda.stream(st):
+                for y in ys:
+                    y.fill_(float("nan"))
+                record()
+            torch.cuda.synchronize()
+            for i, (a, b) in enumerate(zip(got, ys)):
+                assert torch.isfinite(a).all(), (rep, i)
+                assert torch.equal(a.view(torch.int16), b.view(torch.int16)), (rep, i)
+        for g in groups:
+            g.close()
+        for w in ws:
+            w.close()
+        del graph
+    finally:
+        torch.cuda.synchronize()
+        ctx.close()
