@@ -622,6 +622,15 @@ def test_group_of_short_products_with_32_row_tiles(ctx):
         w.close()
 
 
+def test_single_item_group_in_tile_list_order(ctx):
+    """A group of one product with many tiles (1564 of 128 x 512): the item
+    comes from the launch parameters rather than the table while the
+    workgroups walk a tile list."""
+    specs = [(512, 256, 200000, np.float16, False)]
+    for w, _, _ in _check_prefill_group(ctx, specs, 2500):
+        w.close()
+
+
 def test_group_of_prefill_products_accumulating_in_tile_list_order(ctx):
     """y += in tile-list order (1412 tiles of 512 columns, enough per
     workgroup for the wide kernel): the epilogue's general path (read y, add,
