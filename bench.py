@@ -64,9 +64,10 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-sweep", action="store_true")
     p.add_argument("--eager", action="store_true", help="launch directly instead of via HIP graphs (counter runs)")
-    p.add_argument("--phase", choices=("all", "decode", "prefill", "qwen"), default="all",
+    p.add_argument("--phase", choices=("all", "decode", "prefill", "qwen", "config0"), default="all",
                    help="decode: only the M=1 group launch and the copy calibration; prefill: only the "
-                        "M=512 launches (both for counter runs); qwen: only the Qwen2.5-0.5B step at M=1 and 64")
+                        "M=512 launches (both for counter runs); qwen: only the Qwen2.5-0.5B step at M=1 and 64; "
+                        "config0: only the single qkv product at M=1")
     p.add_argument("--prefill-group", action="store_true",
                    help="with --phase prefill: the 129 projections as one group launch instead of 129 launches")
     p.add_argument("--prefill-m", type=int, default=512, help="with --phase prefill: rows M of the prefill step")
@@ -377,6 +378,11 @@ def main():
     stream = torch.cuda.Stream()
     if args.phase == "qwen":
         print(json.dumps({"phase": "qwen", "qwen_step": qwen_step(torch, mnb_hip, ctx, stream, args)}), flush=True)
+        ctx.close()
+        return
+    if args.phase == "config0":
+        print(json.dumps({"phase": "config0", "config0_single_qkv": config0_qkv(torch, mnb_hip, ctx, stream, args)}),
+              flush=True)
         ctx.close()
         return
 

@@ -65,15 +65,23 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
             load_scale_row<ScaleT, SPS>(sp + (size_t)st * kTileRows * SPS, sv[t]);
             if constexpr (HAS_ZP) zb[t] = load_zp<ZB>(zpp + (size_t)st * kTileRows * ZB);
             else zb[t] = 0x88888888u;
+            // keep each super-tile's weights and scales together in issue
+            // order: loads complete in order, so super-tile t can be computed
+            // while the later ones are still arriving (the compiler would
+            // otherwise issue every scale after the last weight load)
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
 
     // M1: one coalesced 16-byte load per lane brings the wave's x slice
-    // (issued before the weights, so it is the first to arrive).
+    // (issued before the weights, so it is the first to arrive).  The lane
+    // mask is applied when the slice is written to LDS, not here: a select
+    // on the loaded value would wait for it before the weight loads issue.
+    bool xok = false;
     auto load_x_slice = [&](int c) -> u32x4_t {
         const int k = c * STW * kTileK + 8 * lane;
-        const u32x4_t v = *(const u32x4_t *)(p.x + min(k, p.kx - 8));
-        return (lane < STW * (kTileK / 8) && k < p.kx) ? v : zero4;
+        xok = lane < STW * (kTileK / 8) && k < p.kx;
+        return *(const u32x4_t *)(p.x + min(k, p.kx - 8));
     };
 
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -81,7 +89,7 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
     auto compute_chunk = [&](int c) {
         if constexpr (M1) {
             // wave-private LDS: a wave's LDS accesses complete in order, no barrier needed
-            if (lane < STW * (kTileK / 8)) ((u32x4_t *)xs)[lane] = xv;
+            if (lane < STW * (kTileK / 8)) ((u32x4_t *)xs)[lane] = xok ? xv : zero4;
         }
 #pragma unroll
         for (int t = 0; t < STW; ++t) {
