@@ -861,8 +861,9 @@ int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *
         p.accumulate = (it.flags & MNB_ACCUMULATE) ? 1 : 0;
         host[(size_t)i].first_wg = (int32_t)wgs;
         wgs += g.NT;
-        int waves = (g.ST + 3) / 4;
-        if (waves > 16) waves = 16;
+        const int stw = m1 ? 4 : mnb::kGemvRowsSTW;
+        int waves = (g.ST + stw - 1) / stw;
+        waves = std::min(waves, m1 ? mnb::kGemvMaxWaves : mnb::kGemvMaxWavesRows);
         if (waves > plan.waves) plan.waves = waves;
     }
     if (items[0].M > mnb::kSkinnyMaxM) return group_create_gemm(ctx, count, items, out);

@@ -19,6 +19,9 @@
 
 namespace mnb {
 
+// LDS bytes of one wave's x block when M > 1: 16 rows x 128 k of fp16.
+constexpr int kXBlockBytes = kTileRows * kTileK * 2;
+
 // M1: x has one row, staged once per workgroup in LDS (A operand = x
 // broadcast to all 16 MFMA rows).  !M1: up to 16 rows read from global
 // memory (rows >= M repeat row M-1 and their results are discarded).
@@ -35,8 +38,10 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
     const int wave = threadIdx.x >> 6;
     const int W = blockDim.x >> 6;
     float4_t *red = (float4_t *)smem;                              // [W][64]
-    // M1: each wave's slice of x (STW*128 halves) in a wave-private region
-    _Float16 *xs = (_Float16 *)(smem + (size_t)W * 64 * sizeof(float4_t)) + wave * (STW * kTileK);
+    // wave-private x region after the reduction slots: M1, the wave's slice
+    // of x (STW*128 halves); !M1, one 16-row x block of a super-tile
+    unsigned char *xw = smem + (size_t)W * 64 * sizeof(float4_t) + (size_t)wave * (M1 ? STW * kTileK * 2 : kXBlockBytes);
+    _Float16 *xs = (_Float16 *)xw;
     const int r = lane & 15, gg = lane >> 4;
     const int nchunks = (p.ST + STW - 1) / STW;
 
@@ -44,15 +49,25 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
     const u32x4_t *qp = (const u32x4_t *)p.q_t + tile0 * 64 + lane;
     const ScaleT *sp = (const ScaleT *)p.s_t + (tile0 * kTileRows + r) * SPS;
     const uint8_t *zpp = HAS_ZP ? p.zp_t + (tile0 * kTileRows + r) * ZB : nullptr;
-    const int m = M1 ? 0 : (r < p.M ? r : p.M - 1);
-    const _Float16 *xr = p.x + (size_t)m * p.ldx + 8 * gg;
-    const half8_t zero8 = {};
     const u32x4_t zero4 = {0u, 0u, 0u, 0u};
     const uint32_t k6400 = vgpr_const(0x64006400u);
 
     u32x4_t raw[STW];
     ScaleT sv[STW][SPS];
     uint32_t zb[STW];
+    // !M1: the x rows of each super-tile are loaded row-contiguous -- lane l
+    // brings 16 bytes at k = 8 (l % 16) of row 4 i + l / 16, so one load
+    // covers four whole 256-byte row pieces -- then go through the wave's LDS
+    // block into MFMA operand order.  (Loading the operand order directly
+    // touches 16 rows, 64 bytes each, per load: four times the cache-line
+    // requests for the same bytes.)  Rows >= M repeat row M - 1.
+    u32x4_t xrw[M1 ? 1 : STW][4];
+    const _Float16 *xrow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = 4 * i + (lane >> 4);
+        xrow[i] = p.x + (size_t)(row < p.M ? row : p.M - 1) * p.ldx;
+    }
     // Straight-line loads (no per-lane branches, so the compiler's wait
     // counters stay exact).  A super-tile index past the end is clamped to the
     // last tile: its k range lies at or beyond kx, where x is zero, so the
@@ -61,6 +76,12 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
 #pragma unroll
         for (int t = 0; t < STW; ++t) {
             const int st = min(c * STW + t, p.ST - 1);
+            if constexpr (!M1) {
+                // clamped into the row; pieces at k >= kx are zeroed in LDS
+                const int k = min((c * STW + t) * kTileK + 8 * (lane & 15), p.kx - 8);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xrw[t][i] = *(const u32x4_t *)(xrow[i] + k);
+            }
             raw[t] = gld_nt(qp + (size_t)st * 64);
             load_scale_row<ScaleT, SPS>(sp + (size_t)st * kTileRows * SPS, sv[t]);
             if constexpr (HAS_ZP) zb[t] = load_zp<ZB>(zpp + (size_t)st * kTileRows * ZB);
@@ -98,13 +119,20 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
             if constexpr (M1) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) xa[j] = *(const half8_t *)(xs + t * kTileK + 32 * j + 8 * gg);
-            } else if (kst + kTileK <= p.kx) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) xa[j] = *(const half8_t *)(xr + kst + 32 * j);
             } else {
+                // 16-byte piece (row, chunk) at row * 256 + ((chunk ^ row) % 16) * 16:
+                // eight consecutive lanes of a write (one row, eight chunks) or
+                // of a read (eight rows, one chunk each) hit distinct banks.
+                // The wave's LDS accesses run in order, so the block can be
+                // rewritten for the next super-tile right after these reads.
+                const bool kok = kst + 8 * (lane & 15) < p.kx;
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    xa[j] = kst + 32 * j + 8 * gg < p.kx ? *(const half8_t *)(xr + kst + 32 * j) : zero8;
+                for (int i = 0; i < 4; ++i) {
+                    const int row = 4 * i + (lane >> 4);
+                    *(u32x4_t *)(xw + row * 256 + (((lane & 15) ^ row) & 15) * 16) = kok ? xrw[t][i] : zero4;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xa[j] = *(const half8_t *)(xw + r * 256 + (((4 * j + gg) ^ r) & 15) * 16);
             }
             if constexpr (SPS == 8) {
                 // bs = 16: the lane's 8 k lie in block 2j + gg/2; fold the scale.
@@ -191,7 +219,7 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
 }
 
 template <typename ScaleT, bool HAS_ZP, bool M1, int SPS, int STW>
-__global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
+__global__ __launch_bounds__(M1 ? 64 * kGemvMaxWaves : 64 * kGemvMaxWavesRows) void gemv_kernel(GemvParams p) {
     extern __shared__ __align__(16) unsigned char smem[];
     gemv_tile<ScaleT, HAS_ZP, M1, SPS, STW>(p, blockIdx.x, smem);
 }
@@ -199,7 +227,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(GemvParams p) {
 // A group of independent projections in one launch: workgroup b computes
 // n-tile b - first_wg of item wg_item[b].
 template <typename ScaleT, bool HAS_ZP, bool M1, int SPS, int STW>
-__global__ __launch_bounds__(1024) void gemv_group_kernel(const GroupItem *__restrict__ items,
+__global__ __launch_bounds__(M1 ? 64 * kGemvMaxWaves : 64 * kGemvMaxWavesRows) void gemv_group_kernel(const GroupItem *__restrict__ items,
                                                           const uint16_t *__restrict__ wg_item) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int it = wg_item[blockIdx.x];
@@ -215,10 +243,15 @@ struct GemvLaunch {
 
 template <typename ScaleT, bool HAS_ZP, bool M1, int SPS>
 static hipError_t gemv_stw(const GemvLaunch &L, const GemvParams &p, hipStream_t s) {
-    switch (L.stw) {
-        case 2: hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, M1, SPS, 2>), L.grid, L.block, L.lds, s, p); break;
-        case 4: hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, M1, SPS, 4>), L.grid, L.block, L.lds, s, p); break;
-        default: return hipErrorInvalidValue;
+    if constexpr (!M1) {
+        if (L.stw != kGemvRowsSTW) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, false, SPS, kGemvRowsSTW>), L.grid, L.block, L.lds, s, p);
+    } else {
+        switch (L.stw) {
+            case 2: hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, true, SPS, 2>), L.grid, L.block, L.lds, s, p); break;
+            case 4: hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, true, SPS, 4>), L.grid, L.block, L.lds, s, p); break;
+            default: return hipErrorInvalidValue;
+        }
     }
     return hipGetLastError();
 }
@@ -241,9 +274,12 @@ static hipError_t gemv_zp(const WeightGeom &g, const GemvLaunch &L, const GemvPa
 }
 
 // Super-tiles per wave: 4 (4 KiB of weights in flight per wave), or 2 when
-// the grid would otherwise have fewer than 8 waves per CU.  K above
-// 16 waves x 4 x 128 = 8192 loops over further chunks per wave.
-static int gemv_stw_for(const WeightGeom &g, int cu_count) {
+// the grid would otherwise have fewer than 8 waves per CU.  M > 1 always
+// takes 2 (kGemvRowsSTW): each super-tile also holds 16 registers of x rows.
+// K above 16 waves x 4 x 128 = 8192 (12 waves x 2 x 128 = 3072 when M > 1)
+// loops over further chunks per wave.
+static int gemv_stw_for(const WeightGeom &g, int cu_count, bool m1) {
+    if (!m1) return kGemvRowsSTW;
     if ((g.ST + 3) / 4 <= 16 && (int64_t)g.NT * ((g.ST + 3) / 4) >= 8LL * cu_count) return 4;
     if ((g.ST + 1) / 2 <= 16) return 2;
     return 4;
@@ -266,23 +302,23 @@ hipError_t launch_gemv(const mnb_weight *w, const MatmulArgs &a, int32_t cu_coun
     p.y_f16 = a.y_type == MNB_F16;
     p.accumulate = a.accumulate;
     GemvLaunch L;
-    L.stw = gemv_stw_for(g, cu_count > 0 ? cu_count : 256);
-    int waves = (g.ST + L.stw - 1) / L.stw;
-    if (waves > 16) waves = 16;
     const bool m1 = a.M == 1;
+    L.stw = gemv_stw_for(g, cu_count > 0 ? cu_count : 256, m1);
+    int waves = (g.ST + L.stw - 1) / L.stw;
+    waves = min(waves, m1 ? kGemvMaxWaves : kGemvMaxWavesRows);
     L.grid = dim3(g.NT);
     L.block = dim3(64 * waves);
-    L.lds = (size_t)waves * 64 * sizeof(float4_t) + (m1 ? (size_t)waves * L.stw * kTileK * 2 : 0);
+    L.lds = (size_t)waves * 64 * sizeof(float4_t) + (size_t)waves * (m1 ? L.stw * kTileK * 2 : kXBlockBytes);
     return g.scale_f32 ? gemv_zp<float>(g, L, p, m1, stream) : gemv_zp<_Float16>(g, L, p, m1, stream);
 }
 
 hipError_t launch_gemv_group(const GemvGroupPlan &g, hipStream_t stream) {
     dim3 grid(g.total_wgs), block(64 * g.waves);
-    const size_t lds = (size_t)g.waves * 64 * sizeof(float4_t) + (g.m1 ? (size_t)g.waves * 4 * kTileK * 2 : 0);
+    const size_t lds = (size_t)g.waves * 64 * sizeof(float4_t) + (size_t)g.waves * (g.m1 ? 4 * kTileK * 2 : kXBlockBytes);
     const GroupItem *it = (const GroupItem *)g.items;
     const uint16_t *wi = (const uint16_t *)g.wg_item;
 #define MNB_GROUP_LAUNCH(ST_, ZP_, M1_, SPS_)                                                                      \
-    hipLaunchKernelGGL((gemv_group_kernel<ST_, ZP_, M1_, SPS_, 4>), grid, block, lds, stream, it, wi)
+    hipLaunchKernelGGL((gemv_group_kernel<ST_, ZP_, M1_, SPS_, M1_ ? 4 : kGemvRowsSTW>), grid, block, lds, stream, it, wi)
 #define MNB_GROUP_SPS(ST_, ZP_, M1_)                              \
     switch (g.sps) {                                              \
         case 1: MNB_GROUP_LAUNCH(ST_, ZP_, M1_, 1); break;        \

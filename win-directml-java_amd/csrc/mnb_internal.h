@@ -206,5 +206,12 @@ hipError_t launch_gemm_group(const GemmGroupPlan &g, float *ws, hipStream_t stre
 
 // largest M handled by the skinny (GEMV-style) kernel
 constexpr int kSkinnyMaxM = 16;
+// waves per workgroup of the GEMV-style kernel: 16, or 12 for M > 1, whose
+// waves each hold a 4 KiB x block in LDS (dynamic LDS stays below 64 KiB;
+// the waves loop over further K chunks)
+constexpr int kGemvMaxWaves = 16, kGemvMaxWavesRows = 12;
+// super-tiles per wave of the GEMV-style kernel for M > 1 (groups and single
+// products alike)
+constexpr int kGemvRowsSTW = 2;
 
 }  // namespace mnb
