@@ -206,6 +206,24 @@ def test_config4_asymmetric_tails(ctx, M, bs, K, N):
     w.close()
 
 
+@pytest.mark.parametrize("M", [2, 3, 4, 6, 8, 9, 12, 16])
+def test_multi_row_products_by_row_group(ctx, M):
+    """Single products with 1 < M <= 16 load the x rows in groups of four
+    (one group up to M = 4, two up to 8, four above); rows past M feed
+    discarded results.  Shapes: whole super-tiles, a K tail with zero points
+    and fp32 scales, and K = 8192, where 12 waves loop over 32 K chunks."""
+    cases = [(3072, 200, 32, False, False), (1000, 130, 128, True, True), (8192, 48, 64, False, False)]
+    for ci, (K, N, bs, zp, f32) in enumerate(cases):
+        t = synth.make_weight(6100 + 10 * M + ci, N, K, bs, with_zp=zp)
+        x16 = synth.make_x(6200 + 10 * M + ci, M, K)
+        y_ref, wmax = oracle_matmul(t, x16)
+        w = upload(ctx, t, as_f32_scales=f32)
+        label = "rows M=%d K=%d N=%d bs=%d zp=%d f32=%d" % (M, K, N, bs, zp, f32)
+        say(label)
+        assert_parity(w.matmul(x16, out_dtype=np.float16), y_ref, x16, t, wmax, True, label)
+        w.close()
+
+
 @pytest.mark.parametrize("bs", [16, 256])
 def test_block_sizes_16_and_256(ctx, bs):
     t = synth.make_weight(77 + bs, 200, 1024, bs, with_zp=True)

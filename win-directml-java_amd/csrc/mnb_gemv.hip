@@ -24,13 +24,14 @@ constexpr int kXBlockBytes = kTileRows * kTileK * 2;
 
 // M1: x has one row, staged once per workgroup in LDS (A operand = x
 // broadcast to all 16 MFMA rows).  !M1: up to 16 rows read from global
-// memory (rows >= M repeat row M-1 and their results are discarded).
+// memory (rows >= M repeat row M-1 and their results are discarded); XR of
+// the 4 groups of 4 rows are loaded (M <= 4 XR), the others are zero.
 // STW: super-tiles per wave; all of a wave's weight, scale and zero-point
 // loads are issued before any arithmetic.
 // One workgroup computes the 16 outputs of n-tile `nt` (per activation row):
 // its W waves take chunks of STW super-tiles; waves beyond the chunk count
 // only take part in the final LDS reduction.
-template <typename ScaleT, bool HAS_ZP, bool M1, int SPS, int STW>
+template <typename ScaleT, bool HAS_ZP, bool M1, int SPS, int STW, int XR = 4>
 __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, unsigned char *smem) {
     constexpr int ZB = SPS <= 2 ? 1 : SPS / 2;
 
@@ -79,8 +80,10 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
             if constexpr (!M1) {
                 // clamped into the row; pieces at k >= kx are zeroed in LDS
                 const int k = min((c * STW + t) * kTileK + 8 * (lane & 15), p.kx - 8);
+                // XR groups of 4 rows are loaded (M <= 4 XR); the rest only
+                // feed results that are discarded and stay zero
 #pragma unroll
-                for (int i = 0; i < 4; ++i) xrw[t][i] = *(const u32x4_t *)(xrow[i] + k);
+                for (int i = 0; i < 4; ++i) xrw[t][i] = i < XR ? *(const u32x4_t *)(xrow[i] + k) : zero4;
             }
             raw[t] = gld_nt(qp + (size_t)st * 64);
             load_scale_row<ScaleT, SPS>(sp + (size_t)st * kTileRows * SPS, sv[t]);
@@ -218,10 +221,10 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
     }
 }
 
-template <typename ScaleT, bool HAS_ZP, bool M1, int SPS, int STW>
+template <typename ScaleT, bool HAS_ZP, bool M1, int SPS, int STW, int XR>
 __global__ __launch_bounds__(M1 ? 64 * kGemvMaxWaves : 64 * kGemvMaxWavesRows) void gemv_kernel(GemvParams p) {
     extern __shared__ __align__(16) unsigned char smem[];
-    gemv_tile<ScaleT, HAS_ZP, M1, SPS, STW>(p, blockIdx.x, smem);
+    gemv_tile<ScaleT, HAS_ZP, M1, SPS, STW, XR>(p, blockIdx.x, smem);
 }
 
 // A group of independent projections in one launch: workgroup b computes
@@ -245,11 +248,17 @@ template <typename ScaleT, bool HAS_ZP, bool M1, int SPS>
 static hipError_t gemv_stw(const GemvLaunch &L, const GemvParams &p, hipStream_t s) {
     if constexpr (!M1) {
         if (L.stw != kGemvRowsSTW) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, false, SPS, kGemvRowsSTW>), L.grid, L.block, L.lds, s, p);
+        // x row groups to load: one per 4 rows of M
+        if (p.M <= 4)
+            hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, false, SPS, kGemvRowsSTW, 1>), L.grid, L.block, L.lds, s, p);
+        else if (p.M <= 8)
+            hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, false, SPS, kGemvRowsSTW, 2>), L.grid, L.block, L.lds, s, p);
+        else
+            hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, false, SPS, kGemvRowsSTW, 4>), L.grid, L.block, L.lds, s, p);
     } else {
         switch (L.stw) {
-            case 2: hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, true, SPS, 2>), L.grid, L.block, L.lds, s, p); break;
-            case 4: hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, true, SPS, 4>), L.grid, L.block, L.lds, s, p); break;
+            case 2: hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, true, SPS, 2, 4>), L.grid, L.block, L.lds, s, p); break;
+            case 4: hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, true, SPS, 4, 4>), L.grid, L.block, L.lds, s, p); break;
             default: return hipErrorInvalidValue;
         }
     }
