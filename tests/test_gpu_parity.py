@@ -617,6 +617,21 @@ def test_random_prefill_groups(ctx, seed):
         w.close()
 
 
+@pytest.mark.parametrize("ms", [(3, 2), (6, 3), (13, 2, 8)])
+def test_small_groups_of_multi_row_products(ctx, ms):
+    """Groups with 1 < M <= 16 and few 32 x 512 tiles run one workgroup per
+    n-tile of each item; the x row groups loaded follow the largest M of the
+    group (one group of four rows up to M = 4, two up to 8, four above), and
+    items with fewer rows still drop their rows past M.  K tails, N tails,
+    fp16 and fp32 outputs, and a group with y +=."""
+    shapes = [(3072, 3072, np.float16), (1000, 500, np.float32), (8192, 700, np.float16)]
+    specs = [(M, K, N, ydt, False) for M, (K, N, ydt) in zip(ms, shapes)]
+    specs.append((ms[-1], 2048, 300, np.float32, True))
+    assert sum((N + 511) // 512 for M, K, N, _, _ in specs) < 1024
+    for w, _, _ in _check_prefill_group(ctx, specs, 2500 + sum(ms)):
+        w.close()
+
+
 def test_group_of_skinny_products_as_weight_stream(ctx):
     """A large group with 1 < M <= 16 (1115 tiles of 32 x 512) runs on the
     GEMM kernel with 32-row tiles in tile-list order: M of 2, 7, 9 and 16

@@ -865,6 +865,7 @@ int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *
         int waves = (g.ST + stw - 1) / stw;
         waves = std::min(waves, m1 ? mnb::kGemvMaxWaves : mnb::kGemvMaxWavesRows);
         if (waves > plan.waves) plan.waves = waves;
+        plan.max_m = std::max(plan.max_m, it.M);
     }
     if (items[0].M > mnb::kSkinnyMaxM) return group_create_gemm(ctx, count, items, out);
     // 1 < M <= 16 with many 32 x 512 tiles: the GEMM's weight stream (x

@@ -229,13 +229,13 @@ __global__ __launch_bounds__(M1 ? 64 * kGemvMaxWaves : 64 * kGemvMaxWavesRows) v
 
 // A group of independent projections in one launch: workgroup b computes
 // n-tile b - first_wg of item wg_item[b].
-template <typename ScaleT, bool HAS_ZP, bool M1, int SPS, int STW>
+template <typename ScaleT, bool HAS_ZP, bool M1, int SPS, int STW, int XR>
 __global__ __launch_bounds__(M1 ? 64 * kGemvMaxWaves : 64 * kGemvMaxWavesRows) void gemv_group_kernel(const GroupItem *__restrict__ items,
                                                           const uint16_t *__restrict__ wg_item) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int it = wg_item[blockIdx.x];
     const GemvParams p = items[it].p;
-    gemv_tile<ScaleT, HAS_ZP, M1, SPS, STW>(p, (int)blockIdx.x - items[it].first_wg, smem);
+    gemv_tile<ScaleT, HAS_ZP, M1, SPS, STW, XR>(p, (int)blockIdx.x - items[it].first_wg, smem);
 }
 
 struct GemvLaunch {
@@ -326,8 +326,14 @@ hipError_t launch_gemv_group(const GemvGroupPlan &g, hipStream_t stream) {
     const size_t lds = (size_t)g.waves * 64 * sizeof(float4_t) + (size_t)g.waves * (g.m1 ? 4 * kTileK * 2 : kXBlockBytes);
     const GroupItem *it = (const GroupItem *)g.items;
     const uint16_t *wi = (const uint16_t *)g.wg_item;
-#define MNB_GROUP_LAUNCH(ST_, ZP_, M1_, SPS_)                                                                      \
-    hipLaunchKernelGGL((gemv_group_kernel<ST_, ZP_, M1_, SPS_, M1_ ? 4 : kGemvRowsSTW>), grid, block, lds, stream, it, wi)
+    // M > 1: x row groups to load, from the largest M of the items
+    const int xr = g.m1 || g.max_m > 8 ? 4 : g.max_m > 4 ? 2 : 1;
+#define MNB_GROUP_XR(ST_, ZP_, M1_, SPS_, XR_) \
+    hipLaunchKernelGGL((gemv_group_kernel<ST_, ZP_, M1_, SPS_, M1_ ? 4 : kGemvRowsSTW, XR_>), grid, block, lds, stream, it, wi)
+#define MNB_GROUP_LAUNCH(ST_, ZP_, M1_, SPS_)                                    \
+    if (M1_ || xr == 4) { MNB_GROUP_XR(ST_, ZP_, M1_, SPS_, 4); }                \
+    else if (xr == 2) { MNB_GROUP_XR(ST_, ZP_, M1_, SPS_, (M1_ ? 4 : 2)); }      \
+    else { MNB_GROUP_XR(ST_, ZP_, M1_, SPS_, (M1_ ? 4 : 1)); }
 #define MNB_GROUP_SPS(ST_, ZP_, M1_)                              \
     switch (g.sps) {                                              \
         case 1: MNB_GROUP_LAUNCH(ST_, ZP_, M1_, 1); break;        \
@@ -345,6 +351,7 @@ hipError_t launch_gemv_group(const GemvGroupPlan &g, hipStream_t stream) {
     }
 #undef MNB_GROUP_SPS
 #undef MNB_GROUP_LAUNCH
+#undef MNB_GROUP_XR
     return hipGetLastError();
 }
 

@@ -157,6 +157,7 @@ struct GemvGroupPlan {
     void *wg_item = nullptr;   // device uint16_t[total_wgs]: item of each workgroup (M > 1)
     int32_t count = 0, total_wgs = 0, waves = 0;
     int32_t scale_f32 = 0, has_zp = 0, sps = 0, m1 = 0;
+    int32_t max_m = 0;         // largest M of the items (M > 1: x row groups to load)
     // M == 1: persistent streaming schedule
     void *units = nullptr;       // device uint32_t[U]: (item << 16) | n-tile, grouped by wave
     void *wave_begin = nullptr;  // device int32_t[stream_wgs * 4 + 1]: first unit of each wave
