@@ -632,6 +632,19 @@ def test_small_groups_of_multi_row_products(ctx, ms):
         w.close()
 
 
+def test_group_of_products_with_64_row_tiles(ctx):
+    """A large group with 32 < M <= 64 (1115 tiles of 64 x 512) runs on the
+    GEMM kernel with 64-row tiles in tile-list order: M of 64, 33, 48 and 40
+    (rows past M clamped and dropped), k tails (K = 200, 1000), N tails, fp16
+    and fp32 outputs; each item is also checked against its own single
+    launch (128-row tiles)."""
+    specs = [(64, 256, 200000, np.float16, False), (33, 200, 150001, np.float32, False),
+             (48, 1000, 120000, np.float16, False), (40, 64, 100000, np.float16, False)]
+    assert sum((N + 511) // 512 for M, K, N, _, _ in specs) == 1115
+    for w, _, _ in _check_prefill_group(ctx, specs, 2700):
+        w.close()
+
+
 def test_group_of_skinny_products_as_weight_stream(ctx):
     """A large group with 1 < M <= 16 (1115 tiles of 32 x 512) runs on the
     GEMM kernel with 32-row tiles in tile-list order: M of 2, 7, 9 and 16

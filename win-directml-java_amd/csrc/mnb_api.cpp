@@ -689,11 +689,14 @@ struct mnb_group {
 
 // Whole tiles per workgroup from which a GEMM group runs in tile-list order.
 constexpr int kGemmListTilesPerWg = 4;
-// Largest M of a group's items for 32-row tiles.
-constexpr int kGemmSkinnyMaxM = 32;
+// Largest M of a group's items for 32-row tiles, and for 64-row tiles.
+constexpr int kGemmSkinnyMaxM = 32, kGemmHalfMaxM = 64;
 // Cost of a 512-column stage in 256-column stages (same-box A/B of the M=512
 // group: 1046 vs 1155 TFLOP/s, so 2 / 1.105).
 constexpr double kGemmWideStageCost = 1.81;
+// Cost of a 64 x 512 stage in 128 x 256 stages: the same MFMA work and the
+// same operand bytes (x and weights trade places), rounded up.
+constexpr double kGemmHalfStageCost = 1.1;
 
 // A group of products with M > 16: one launch over one workgroup per CU,
 // the items' (tile, stage) iterations in stream-K order or, for many tiles,
@@ -759,13 +762,32 @@ static int32_t group_create_gemm(mnb_context *ctx, int32_t count, const mnb_grou
         for (int32_t g = 0; g < plan.G; ++g) m = std::max<int64_t>(m, r[(size_t)g + 1].iter - r[(size_t)g].iter);
         return m;
     };
-    // Rows of at most 32 per item: 32-row tiles of 512 columns (a weight
-    // stream; 128-row tiles would multiply by up to 8 the MFMA work).
+    // Rows of at most 32 (64) per item: 32-row (64-row) tiles of 512 columns
+    // (128-row tiles would multiply by up to 8 (2) the MFMA work).
     int32_t max_m = 0;
     for (int32_t i = 0; i < count; ++i) max_m = std::max(max_m, items[i].M);
-    if (max_m <= kGemmSkinnyMaxM && mnb::sk_wide_supported(plan.scale_f32, plan.sps) &&
-        build(mnb::kGemmWideNTW, mnb::kGemmSkinnyFM) && tiles >= min_tiles) {
+    const bool wide_ok = mnb::sk_wide_supported(plan.scale_f32, plan.sps);
+    // 64-row tiles take half the stages of 128-row tiles at about the same
+    // cost each; they need no split, so they run in tile-list order, chosen
+    // when the busiest workgroup's stages beat the 128-row plan's average
+    // (its best case); leaves the list in seq/wg when chosen
+    auto half_wins = [&]() {
+        int64_t narrow_iters = 0;
+        for (int32_t i = 0; i < count; ++i) {
+            const WeightGeom &g = items[i].weight->g;
+            narrow_iters += (int64_t)mnb::sk_tiles(items[i].M, g.NT, mnb::kGemmNTW, mnb::kGemmFM) * g.ST;
+        }
         mnb::sk_tile_list(plan.host, plan.G, seq, wg);
+        if ((double)busiest(wg) * kGemmHalfStageCost < (double)narrow_iters / plan.G) return true;
+        seq.clear();
+        wg.clear();
+        return false;
+    };
+    if (max_m <= kGemmSkinnyMaxM && wide_ok && build(mnb::kGemmWideNTW, mnb::kGemmSkinnyFM) && tiles >= min_tiles) {
+        mnb::sk_tile_list(plan.host, plan.G, seq, wg);
+    } else if (max_m <= kGemmHalfMaxM && wide_ok && build(mnb::kGemmWideNTW, mnb::kGemmHalfFM) && tiles >= plan.G &&
+               half_wins()) {
+        // 64 x 512 tiles in tile-list order
     } else if (!build(mnb::kGemmNTW)) {
         return fail(MNB_ERR_INVALID_ARGUMENT, "group too large");
     } else if (tiles >= min_tiles) {

@@ -42,9 +42,11 @@
 //   side; no tile is split.  These launches may use 512-column tiles (8 waves
 //   of 128 x 64, a two-slot ring), which halve the LDS reads of x per MFMA,
 //   and stage whole fp16 output tiles through LDS so that each store writes
-//   16 rows x 64 bytes; and, for groups whose M is at most 32 (down to
-//   M = 2), 32 x 512 tiles (one 32-row fragment per wave, a three-slot ring):
-//   then the kernel is a weight stream whose x rows are shared in LDS.
+//   16 rows x 64 bytes; for groups whose M is at most 32 (down to M = 2),
+//   32 x 512 tiles (one 32-row fragment per wave, a three-slot ring): then
+//   the kernel is a weight stream whose x rows are shared in LDS; and for
+//   groups whose M is at most 64, 64 x 512 tiles (two 32-row fragments per
+//   wave, a three-slot ring), half the MFMA work of 128-row tiles.
 // Logical workgroup ids are laid out XCD-contiguous, so neighbouring
 // workgroups (which share tiles and weight columns) sit on the same XCD.
 #include <algorithm>
@@ -60,6 +62,7 @@ constexpr int kSkBN = kSkWaves * kSkNTW * kTileRows;   // 256 columns per tile
 constexpr int kSkWideNTW = kGemmWideNTW;   // wide tiles (tile-list launches only): 64 columns per wave, 512 per tile
 constexpr int kSkFM = kSkBM / 32;   // 32-row A fragments per wave
 constexpr int kSkSkinnyFM = kGemmSkinnyFM;   // skinny tiles (tile-list launches only): 32 rows
+constexpr int kSkHalfFM = kGemmHalfFM;       // half-height tiles (tile-list launches only): 64 rows
 constexpr int kSkThreads = 64 * kSkWaves;
 constexpr int kSkPartialFloats = kSkBM * kSkBN;   // one fp32 partial tile, [kSkBM][kSkBN] row-major
 constexpr int kSkReduceRows = 16;                 // rows of a partial tile per reduce workgroup
@@ -269,7 +272,7 @@ struct SkSlot {
 template <typename ScaleT, bool HAS_ZP, int SPS, int NTW, int FM>
 __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     using L = SkSlot<ScaleT, HAS_ZP, SPS, NTW, FM>;
-    constexpr int BM = L::BM;                        // rows per tile (128, or 32 for skinny tiles)
+    constexpr int BM = L::BM;                        // rows per tile (128, 64, or 32 for skinny tiles)
     constexpr int BN = kSkWaves * NTW * kTileRows;   // columns per tile
     constexpr int FN = NTW / 2;                      // 32-column weight fragments per wave
     constexpr int ZB = L::ZB;
@@ -516,7 +519,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             }
         } else if constexpr (NTW == kSkNTW && FM == kSkFM) {
             // partial tile of a split tile: [BM][kSkBN] fp32, summed by sk_reduce_kernel
-            // (wide and skinny tiles run in tile-list order only, where no tile is split)
+            // (wide, half and skinny tiles run in tile-list order only, where no tile is split)
             const int slot = first_seg ? 0 : 1;
             __attribute__((address_space(1))) float *part =
                 (__attribute__((address_space(1))) float *)p.ws + ((size_t)g * 2 + slot) * kSkPartialFloats;
@@ -854,6 +857,8 @@ static void launch_sk_variant(int ntw, int fm, dim3 grid, dim3 block, hipStream_
     } else if constexpr (kSkWideNTW * kTileRows * SPS * sizeof(ScaleT) <= 1024) {
         if (fm == kSkFM)
             hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, kSkWideNTW, kSkFM>), grid, block, 0, stream, p);
+        else if (fm == kSkHalfFM)
+            hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, kSkWideNTW, kSkHalfFM>), grid, block, 0, stream, p);
         else
             hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, kSkWideNTW, kSkSkinnyFM>), grid, block, 0, stream, p);
     }
@@ -866,10 +871,10 @@ static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem
                             const SkTile *seq, const SkRange *wg, int ntw, int fm, int64_t iters, int scale_f32,
                             int has_zp, int sps, int G, float *ws, hipStream_t stream) {
     if (iters >= (int64_t)1 << 31 || G < 1 || G > kSkReduceThreads) return hipErrorInvalidValue;
-    // 256 x 128 tiles, or wide (512 x 128) and skinny (512 x 32) tiles in
+    // 256 x 128 tiles, or wide (512 x 128), half (512 x 64) and skinny (512 x 32) tiles in
     // tile-list order only (no split tiles, no partial tiles)
     const bool narrow = ntw == kSkNTW && fm == kSkFM;
-    const bool wide = ntw == kSkWideNTW && (fm == kSkFM || fm == kSkSkinnyFM);
+    const bool wide = ntw == kSkWideNTW && (fm == kSkFM || fm == kSkHalfFM || fm == kSkSkinnyFM);
     if (!narrow && (!wide || !seq || !sk_wide_supported(scale_f32, sps))) return hipErrorInvalidValue;
     SkParams p;
     p.one = one;

@@ -173,7 +173,7 @@ constexpr int kStreamWavesPerBlock = 4;
 // (128 rows), or 1 (32-row skinny tiles, with 512 columns, in tile-list
 // order only)
 constexpr int kGemmNTW = 2, kGemmWideNTW = 4;
-constexpr int kGemmFM = 4, kGemmSkinnyFM = 1;
+constexpr int kGemmFM = 4, kGemmHalfFM = 2, kGemmSkinnyFM = 1;
 
 // A recorded group of independent products with M > 16 (all items share the
 // kernel variant): one launch over all their iterations, in stream-K order
