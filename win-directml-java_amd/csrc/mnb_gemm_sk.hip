@@ -63,6 +63,9 @@ constexpr int kSkWideNTW = kGemmWideNTW;   // wide tiles (tile-list launches onl
 constexpr int kSkFM = kSkBM / 32;   // 32-row A fragments per wave
 constexpr int kSkSkinnyFM = kGemmSkinnyFM;   // skinny tiles (tile-list launches only): 32 rows
 constexpr int kSkHalfFM = kGemmHalfFM;       // half-height tiles (tile-list launches only): 64 rows
+// Epilogue staging of 512-column tiles: per wave one 32 x 32 fp16 block,
+// rows padded to 80 bytes against bank conflicts.
+constexpr int kSkStageRow = 80, kSkStageWave = 32 * kSkStageRow, kSkStageBytes = kSkWaves * kSkStageWave;
 constexpr int kSkThreads = 64 * kSkWaves;
 constexpr int kSkPartialFloats = kSkBM * kSkBN;   // one fp32 partial tile, [kSkBM][kSkBN] row-major
 constexpr int kSkReduceRows = 16;                 // rows of a partial tile per reduce workgroup
@@ -259,7 +262,10 @@ struct SkSlot {
     static constexpr int kTileZ = kTileRows * ZB;
     static constexpr int kZRegion = HAS_ZP ? (kNT * kTileZ > kWin ? kNT * kTileZ : kWin) : 0;
     static constexpr int kBytes = kZ + kZRegion;
-    static constexpr int kDepth = 3 * kBytes <= 160 * 1024 ? 3 : 2;   // ring slots (fits the 160 KiB LDS)
+    // ring slots: three when they fit the 160 KiB LDS beside the epilogue
+    // staging of 512-column tiles, else two (the staging pays more than a
+    // third slot: 64 x 512 tiles at K = 896, 113 -> 100 us per Qwen step)
+    static constexpr int kDepth = 3 * kBytes + (NTW == kSkWideNTW ? kSkStageBytes : 0) <= 160 * 1024 ? 3 : 2;
     // per wave and stage: x pieces of 4 rows, its packed tiles, and one
     // 1 KiB window each of the scale and zero-point regions that contains
     // the wave's own tiles (all 64 lanes load: no lane mask, no branch)
@@ -278,11 +284,10 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     constexpr int ZB = L::ZB;
     constexpr int D = L::kDepth;
     __shared__ __align__(1024) unsigned char ring[D][L::kBytes];
-    // Epilogue staging (wide tiles, where the LDS has room): per wave one
-    // 32 x 32 fp16 block, rows padded to 80 bytes against bank conflicts.
-    constexpr int kStageRow = 80, kStageWave = 32 * kStageRow;
-    constexpr bool kStaged = NTW == kSkWideNTW && D * L::kBytes + kSkWaves * kStageWave <= 160 * 1024;
-    __shared__ __align__(16) unsigned char stage_all[kStaged ? kSkWaves * kStageWave : 16];
+    // Epilogue staging (512-column tiles, where the LDS has room)
+    constexpr int kStageRow = kSkStageRow, kStageWave = kSkStageWave;
+    constexpr bool kStaged = NTW == kSkWideNTW && D * L::kBytes + kSkStageBytes <= 160 * 1024;
+    __shared__ __align__(16) unsigned char stage_all[kStaged ? kSkStageBytes : 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
