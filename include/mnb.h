@@ -218,7 +218,8 @@ int32_t mnb_max_batch_rows(void);
  * (prefill-shaped products: one GEMM launch over all items' tiles).  A GEMM
  * group with few tiles splits tiles across workgroups (stream-K) and then
  * uses the context's GEMM workspace, so it must not overlap other M > 16
- * calls on the context; a group with many tiles (also one of 1 < M <= 16)
+ * calls on the context; a group with many tiles (also one of 1 < M <= 16),
+ * or whose items have M <= 64 and whose 64-row tiles balance well enough,
  * gives each workgroup whole tiles and uses no workspace.  The group keeps
  * its own device descriptor table, so mnb_group_run allocates nothing and can
  * be captured in a HIP graph. */
