@@ -95,17 +95,20 @@ def test_graph_capture_replays_match_eager():
 
 def test_graph_capture_of_tile_list_groups():
     """Group launches in tile-list order (a prefill group with 512-column
-    tiles and a 1 < M <= 16 group on 32-row tiles) captured into one HIP
-    graph; every replay, with new activations written between replays,
-    equals the eager launches bit for bit."""
+    tiles, a 32 < M <= 64 group on 64-row tiles and a 1 < M <= 16 group on
+    32-row tiles) captured into one HIP graph; every replay, with new
+    activations written between replays, equals the eager launches bit for
+    bit."""
     import torch
     ctx = mnb_hip.Context(0)
     try:
         dev = "cuda"
         gen = torch.Generator(device=dev).manual_seed(11)
         groups, xs, ys, ws = [], [], [], []
-        # 1344 tiles of 128 x 512 and 1075 tiles of 32 x 512: both run in tile-list order
+        # 1344 tiles of 128 x 512, 316 of 64 x 512 (K = 896: 7 stages each, fewer
+        # than 4 per workgroup) and 1075 of 32 x 512: all run in tile-list order
         for gi, (M, shapes) in enumerate([(512, [(3072, 16384), (3072, 9216), (8192, 3072)] * 6),
+                                           (48, [(896, 151936), (896, 9728)]),
                                            (8, [(256, 200000), (512, 200000), (128, 150000)])]):
             items = []
             for i, (K, N) in enumerate(shapes):
