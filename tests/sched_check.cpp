@@ -1,8 +1,13 @@
-// Checks the tile-list schedule of a grouped prefill GEMM (mnb::sk_tile_list)
-// on the CPU.  Input (stdin): G, then one line "MT NG ST" per item.  Exits 1
-// on the first broken invariant; prints balance and locality figures.
+// Checks the schedules of a group launch on the CPU.  Input (stdin):
+//   tile list of a grouped prefill GEMM (mnb::sk_tile_list): G, then one line
+//     "MT NG ST" per item;
+//   streaming M = 1 schedule (mnb::stream_schedule): the word "stream", the
+//     wave count, then one line "NT ST" per item.
+// Exits 1 on the first broken invariant; prints balance (and, for the tile
+// list, locality) figures.
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include <algorithm>
 #include <set>
@@ -17,9 +22,67 @@ static int fail(const char *what, long a, long b) {
     return 1;
 }
 
+// Every (item, n-tile) unit exactly once, each wave's units in group order,
+// the wave table consistent with the units, and the longest-first bound:
+// no wave carries more than the mean cost plus one unit.
+static int check_stream() {
+    long waves = 0;
+    if (scanf("%ld", &waves) != 1 || waves < 1) return fail("input", waves, 0);
+    std::vector<int32_t> NT, ST;
+    int nt, st;
+    while (scanf("%d %d", &nt, &st) == 2) {
+        NT.push_back(nt);
+        ST.push_back(st);
+    }
+    std::vector<uint32_t> units;
+    std::vector<int32_t> wb;
+    if (!stream_schedule(NT, ST, waves, units, wb)) {
+        printf("refused\n");
+        return 0;
+    }
+    long total = 0, cost = 0, maxunit = 0;
+    for (size_t i = 0; i < NT.size(); ++i) {
+        total += NT[i];
+        cost += (long)NT[i] * (ST[i] + 1);
+        maxunit = std::max<long>(maxunit, ST[i] + 1);
+    }
+    if ((long)units.size() != total) return fail("unit count", (long)units.size(), total);
+    if ((long)wb.size() != 2 * waves + 1) return fail("wave table size", (long)wb.size(), 2 * waves + 1);
+    std::vector<std::vector<char>> seen(NT.size());
+    for (size_t i = 0; i < NT.size(); ++i) seen[i].assign((size_t)NT[i], 0);
+    long maxcost = 0, busy = 0;
+    for (long w = 0; w < waves; ++w) {
+        const long b = wb[(size_t)(2 * w)], e = wb[(size_t)(2 * w + 2)];
+        if (b > e || e > (long)units.size()) return fail("wave range", b, e);
+        if (w == 0 && b != 0) return fail("first wave start", b, 0);
+        long jobs = 0, c = 0;
+        for (long k = b; k < e; ++k) {
+            const uint32_t u = units[(size_t)k];
+            const size_t it = u >> 16, t = u & 0xFFFFu;
+            if (it >= NT.size() || (long)t >= NT[it]) return fail("unit code", (long)it, (long)t);
+            if (seen[it][t]++) return fail("unit twice", (long)it, (long)t);
+            if (k > b && units[(size_t)k - 1] >= u) return fail("wave order", w, k);
+            jobs += ST[it];
+            c += ST[it] + 1;
+        }
+        if (jobs != wb[(size_t)(2 * w + 1)]) return fail("wave super-tiles", w, jobs);
+        maxcost = std::max(maxcost, c);
+        busy += e > b;
+    }
+    if (wb[(size_t)(2 * waves)] != (long)units.size()) return fail("end of list", wb[(size_t)(2 * waves)], (long)units.size());
+    const double mean = (double)cost / (double)waves;
+    if ((double)maxcost > mean + (double)maxunit) return fail("longest-first bound", maxcost, (long)mean);
+    printf("ok units=%ld waves=%ld busy=%ld max_wave_cost=%ld mean=%.1f imbalance=%.4f\n", total, waves, busy, maxcost,
+           mean, (double)maxcost / mean - 1.0);
+    return 0;
+}
+
 int main() {
-    int G = 0;
-    if (scanf("%d", &G) != 1 || G < 1) return fail("input", G, 0);
+    char first[32] = {0};
+    if (scanf("%31s", first) != 1) return fail("input", 0, 0);
+    if (strcmp(first, "stream") == 0) return check_stream();
+    const int G = atoi(first);
+    if (G < 1) return fail("input", G, 0);
     std::vector<SkItem> items;
     int MT, NG, ST;
     long ibeg = 0;

@@ -1,5 +1,7 @@
-"""Tile-list schedule of a grouped prefill GEMM (mnb::sk_tile_list in
-win-directml-java_amd/csrc/mnb_sched.cpp), checked on the CPU.
+"""Schedules of group launches (win-directml-java_amd/csrc/mnb_sched.cpp),
+checked on the CPU: the tile list of a grouped prefill GEMM
+(mnb::sk_tile_list) and the static unit lists of the M = 1 streaming kernel
+(mnb::stream_schedule).
 
 The grouped launch replaces a sequence of the reference's batched GEMM
 dispatches (INT4_MATMUL_BATCH_TILED_HLSL, MatMulNBitsKernel.java:732-820,
@@ -73,3 +75,52 @@ def test_random_groups(checker, seed):
 def test_more_workgroups_than_tiles(checker):
     f = run(checker, 256, [(1, 3, 24), (2, 1, 5)])
     assert f["tiles"] == 5
+
+
+# ------------------------------------------------ M = 1 streaming schedule
+
+def run_stream(checker, waves, items):
+    """items: (NT, ST) per item.  Returns the checker's figures (None when refused)."""
+    inp = "stream\n%d\n" % waves + "\n".join("%d %d" % t for t in items) + "\n"
+    r = subprocess.run([checker], input=inp, capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout
+    if r.stdout.startswith("refused"):
+        return None
+    assert r.stdout.startswith("ok"), r.stdout
+    return {k: float(v) for k, v in re.findall(r"(\w+)=([\d.]+)", r.stdout)}
+
+
+def phi3_stream_items():
+    """The Phi-3-mini decode step's 129 M = 1 products: (n-tiles, super-tiles)."""
+    layer = [(3072, 9216), (3072, 3072), (3072, 16384), (8192, 3072)]
+    return [((N + 15) // 16, (K + 127) // 128) for _ in range(32) for K, N in layer] + [((32064 + 15) // 16, 24)]
+
+
+@pytest.mark.parametrize("waves", [256 * 8, 256 * 12, 256 * 16, 1000])
+def test_stream_schedule_of_the_phi3_decode_step(checker, waves):
+    """The headline decode group: 32 x {qkv, o, gate_up, down} + lm_head, 65,492
+    units, far more than the waves, so every wave's pipeline carries across
+    many unit boundaries; every unit is listed once and the busiest wave is
+    within one unit of the mean."""
+    f = run_stream(checker, waves, phi3_stream_items())
+    assert f["units"] == 65492
+    assert f["busy"] == waves
+    assert f["imbalance"] < 0.05
+
+
+def test_stream_schedule_fewer_units_than_waves(checker):
+    f = run_stream(checker, 4096, [(576, 24), (192, 24), (192, 64), (3, 7)])
+    assert f["units"] == 963 and f["busy"] == 963
+
+
+def test_stream_schedule_refuses_oversized_items(checker):
+    assert run_stream(checker, 64, [(65537, 1)]) is None
+    assert run_stream(checker, 64, [(65536, 1)]) is not None
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_stream_schedule_random_groups(checker, seed):
+    rng = np.random.default_rng(100 + seed)
+    waves = int(rng.choice([1, 7, 64, 1024, 3072]))
+    items = [(int(rng.integers(1, 3000)), int(rng.integers(1, 80))) for _ in range(int(rng.integers(1, 60)))]
+    run_stream(checker, waves, items)

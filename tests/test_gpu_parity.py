@@ -11,7 +11,6 @@ Bars (stated per test):
 """
 import os
 import subprocess
-import sys
 
 import numpy as np
 import pytest
@@ -19,13 +18,10 @@ import pytest
 import mnb_hip
 from mnb_hip import synth
 import mnb_oracle as orc
+from parity_util import (THREADS, assert_parity, fp16_ulp, max_abs_w, oracle_inputs, oracle_matmul, say,
+                         upload)
 
 pytestmark = pytest.mark.gpu
-
-
-def say(*a):
-    print(*a, flush=True)
-    sys.stdout.flush()
 
 
 @pytest.fixture(scope="module")
@@ -36,68 +32,6 @@ def ctx():
     say("device:", i.name.decode(), i.arch.decode(), "CUs", i.compute_units)
     yield c
     c.close()
-
-
-THREADS = min(16, len(os.sched_getaffinity(0)))
-
-
-def fp16_ulp(v):
-    a = np.abs(np.asarray(v, np.float64))
-    e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
-    return 2.0 ** (e - 10)
-
-
-def oracle_inputs(t: synth.QuantTensor, rows=None):
-    """Reference-form tensors: fp32 scales (loader widening), flat zero points
-    (runtime layout; 0x88 when absent), optionally restricted to `rows`."""
-    kb, bs = t.kb, t.bs
-    q = t.q.reshape(t.N, kb * bs // 2)
-    s = orc.fp16_bits_to_fp32(t.scales_f16.view(np.uint16)).reshape(t.N, kb)
-    if t.zp_row_padded is not None:
-        zrp = t.zp_row_padded
-    else:
-        zrp = np.full((t.N, (kb + 1) // 2), 0x88, np.uint8)
-    if rows is not None:
-        q, s, zrp = q[rows], s[rows], zrp[rows]
-    n = q.shape[0]
-    z = synth.zp_row_padded_to_flat(zrp, n, kb)
-    return q.reshape(-1), s.reshape(-1), z, n
-
-
-def oracle_matmul(t: synth.QuantTensor, x16: np.ndarray, rows=None):
-    q, s, z, n = oracle_inputs(t, rows)
-    kpad = t.kb * t.bs
-    M = x16.shape[0]
-    x = np.zeros((M, kpad), np.float32)
-    x[:, : t.K] = x16.astype(np.float32)
-    y = orc.matmul(q, s, z, n, kpad, t.bs, x, threads=THREADS)
-    wmax = float(np.max(np.abs(orc.dequantize(q, s, z, n, kpad, t.bs)))) if n * kpad <= 64 << 20 else None
-    return y, wmax
-
-
-def max_abs_w(t: synth.QuantTensor) -> float:
-    """max|w| = max over blocks of scale * max|q - zp| (exact, no dequant needed)."""
-    s = t.scales_f16.astype(np.float32).reshape(t.N, t.kb)
-    return float(np.max(np.abs(s)) * 15.0) if t.zp_row_padded is not None else float(np.max(np.abs(s)) * 8.0)
-
-
-def assert_parity(y, y_ref, x16, t, wmax=None, fp16_out=False, label=""):
-    K = t.K
-    wm = wmax if wmax is not None else max_abs_w(t)
-    tol = 1e-3 * np.sqrt(K) * float(np.max(np.abs(x16.astype(np.float32)))) * wm
-    allowed = tol + (fp16_ulp(y_ref) if fp16_out else 0.0)
-    err = np.abs(y.astype(np.float64) - y_ref.astype(np.float64))
-    worst = float(np.max(err - allowed))
-    say("parity %s: max|err|=%.3e tol=%.3e" % (label, float(np.max(err)), tol))
-    assert np.all(np.isfinite(y)), label
-    assert worst <= 0.0, "%s: max|err| %.3e exceeds bound %.3e" % (label, float(np.max(err)), tol)
-
-
-def upload(ctx, t: synth.QuantTensor, as_f32_scales=False):
-    s = t.scales_f16.astype(np.float32) if as_f32_scales else t.scales_f16
-    if t.zp_row_padded is not None:
-        return mnb_hip.Weight(ctx, t.N, t.K, t.bs, t.q, s, t.zp_row_padded, mnb_hip.MNB_ZP_ROW_PADDED)
-    return mnb_hip.Weight(ctx, t.N, t.K, t.bs, t.q, s)
 
 
 # ------------------------------------------------------------ dequant -----

@@ -15,7 +15,6 @@
 #include <cstring>
 #include <algorithm>
 #include <limits>
-#include <queue>
 #include <string>
 #include <vector>
 
@@ -910,9 +909,8 @@ int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *
     plan.total_wgs = (int32_t)wgs;
     DeviceGuard guard(ctx->device);
 
-    // M == 1: static schedule for the persistent streaming kernel.  Units
-    // (item, n-tile) are assigned longest-first to the least loaded wave, cost
-    // = super-tiles + 1, and each wave keeps its units in group order.
+    // M == 1: static schedule for the persistent streaming kernel (units
+    // dealt longest first to the least loaded wave, mnb_sched.cpp)
     std::vector<uint32_t> units;
     std::vector<int32_t> wave_begin;
     if (plan.m1) {
@@ -922,39 +920,13 @@ int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *
         const int wpc = mnb::stream_kernel_waves_per_cu(plan.scale_f32, plan.has_zp, plan.sps);
         const int64_t total_waves = (int64_t)ctx->cu_count * wpc;
         plan.stream_wgs = (int32_t)(total_waves / mnb::kStreamWavesPerBlock);
-        const int64_t nwaves = (int64_t)plan.stream_wgs * mnb::kStreamWavesPerBlock;
-        std::vector<std::pair<int32_t, uint32_t>> order;   // (cost, code)
-        order.reserve((size_t)wgs);
+        std::vector<int32_t> nt((size_t)count), st((size_t)count);
         for (int32_t i = 0; i < count; ++i) {
-            const WeightGeom &g = items[i].weight->g;
-            for (int32_t nt = 0; nt < g.NT; ++nt) order.emplace_back(g.ST + 1, ((uint32_t)i << 16) | (uint32_t)nt);
+            nt[(size_t)i] = items[i].weight->g.NT;
+            st[(size_t)i] = items[i].weight->g.ST;
         }
-        std::stable_sort(order.begin(), order.end(),
-                         [](const std::pair<int32_t, uint32_t> &a, const std::pair<int32_t, uint32_t> &b) { return a.first > b.first; });
-        typedef std::pair<int64_t, int32_t> Load;   // (cost, wave)
-        std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
-        for (int32_t w = 0; w < (int32_t)nwaves; ++w) heap.push(Load(0, w));
-        std::vector<std::vector<uint32_t>> per((size_t)nwaves);
-        for (const auto &u : order) {
-            Load l = heap.top();
-            heap.pop();
-            per[(size_t)l.second].push_back(u.second);
-            l.first += u.first;
-            heap.push(l);
-        }
-        // per wave: first unit, number of super-tiles of its units; then the end
-        wave_begin.reserve(2 * (size_t)nwaves + 1);
-        units.reserve(order.size());
-        for (auto &v : per) {
-            std::sort(v.begin(), v.end());
-            int64_t jobs = 0;
-            for (uint32_t c : v) jobs += items[c >> 16].weight->g.ST;
-            if (jobs > std::numeric_limits<int32_t>::max()) return fail(MNB_ERR_INVALID_ARGUMENT, "group too large");
-            wave_begin.push_back((int32_t)units.size());
-            wave_begin.push_back((int32_t)jobs);
-            units.insert(units.end(), v.begin(), v.end());
-        }
-        wave_begin.push_back((int32_t)units.size());
+        if (!mnb::stream_schedule(nt, st, (int64_t)plan.stream_wgs * mnb::kStreamWavesPerBlock, units, wave_begin))
+            return fail(MNB_ERR_INVALID_ARGUMENT, "group too large");
     }
 
     hipError_t e;

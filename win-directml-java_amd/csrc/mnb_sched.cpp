@@ -3,6 +3,10 @@
 #include "mnb_sched.h"
 
 #include <algorithm>
+#include <functional>
+#include <limits>
+#include <queue>
+#include <utility>
 
 namespace mnb {
 
@@ -68,6 +72,46 @@ void sk_tile_list(const std::vector<SkItem> &items, int G, std::vector<SkTile> &
         }
     }
     wg[(size_t)G] = SkRange{(int32_t)seq.size(), (int32_t)iter};
+}
+
+bool stream_schedule(const std::vector<int32_t> &NT, const std::vector<int32_t> &ST, int64_t waves,
+                     std::vector<uint32_t> &units, std::vector<int32_t> &wave_begin) {
+    units.clear();
+    wave_begin.clear();
+    if (waves < 1 || NT.size() != ST.size() || NT.size() > 65536) return false;
+    std::vector<std::pair<int32_t, uint32_t>> order;   // (cost, code)
+    for (size_t i = 0; i < NT.size(); ++i) {
+        if (NT[i] < 1 || NT[i] > 65536 || ST[i] < 1) return false;
+        for (int32_t nt = 0; nt < NT[i]; ++nt) order.emplace_back(ST[i] + 1, ((uint32_t)i << 16) | (uint32_t)nt);
+    }
+    std::stable_sort(order.begin(), order.end(),
+                     [](const std::pair<int32_t, uint32_t> &a, const std::pair<int32_t, uint32_t> &b) {
+                         return a.first > b.first;
+                     });
+    typedef std::pair<int64_t, int64_t> Load;   // (cost, wave)
+    std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+    for (int64_t w = 0; w < waves; ++w) heap.push(Load(0, w));
+    std::vector<std::vector<uint32_t>> per((size_t)waves);
+    for (const auto &u : order) {
+        Load l = heap.top();
+        heap.pop();
+        per[(size_t)l.second].push_back(u.second);
+        l.first += u.first;
+        heap.push(l);
+    }
+    wave_begin.reserve(2 * (size_t)waves + 1);
+    units.reserve(order.size());
+    for (auto &v : per) {
+        std::sort(v.begin(), v.end());
+        int64_t jobs = 0;
+        for (uint32_t c : v) jobs += ST[c >> 16];
+        if (jobs > std::numeric_limits<int32_t>::max()) return false;
+        wave_begin.push_back((int32_t)units.size());
+        wave_begin.push_back((int32_t)jobs);
+        units.insert(units.end(), v.begin(), v.end());
+    }
+    wave_begin.push_back((int32_t)units.size());
+    return true;
 }
 
 }  // namespace mnb

@@ -45,4 +45,17 @@ struct SkRange {
 // the iterations [wg[g].iter, wg[g + 1].iter)).
 void sk_tile_list(const std::vector<SkItem> &items, int G, std::vector<SkTile> &seq, std::vector<SkRange> &wg);
 
+// Static schedule of a group of M = 1 products on the persistent streaming
+// kernel (mnb_stream.hip).  A unit is one 16-row n-tile of one item over its
+// whole K, coded (item << 16) | n-tile; item i has NT[i] n-tiles of ST[i]
+// super-tiles.  Units are dealt longest first (cost = super-tiles + 1, the
+// unit's output write counted as one) to the least loaded of `waves` waves;
+// each wave keeps its units in group order.  Fills units (wave-major) and
+// wave_begin (2 * waves + 1 entries: per wave its first unit and the number of
+// super-tiles of its units, then the end of the list).  Returns false when
+// there are 65536 items or more, an item has more than 65536 n-tiles, or a
+// wave's super-tiles do not fit 31 bits.
+bool stream_schedule(const std::vector<int32_t> &NT, const std::vector<int32_t> &ST, int64_t waves,
+                     std::vector<uint32_t> &units, std::vector<int32_t> &wave_begin);
+
 }  // namespace mnb
