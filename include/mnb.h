@@ -19,10 +19,16 @@
  *       MNB_ERR_INVALID_ARGUMENT -> IllegalArgumentException
  *       MNB_ERR_INVALID_STATE    -> IllegalStateException ("Kernel not prepared")
  *       everything else          -> RuntimeException("MatMulNBitsKernel.<op> failed")
- *   - A weight object is not thread-safe for concurrent calls that use host
- *     memory (they share the context's staging buffers), the same as one
- *     reference kernel instance (MNK:77-81).  Calls with device pointers on
- *     distinct streams may run concurrently.
+ *   - Calls on one context share its workspace (the GEMM's split-tile
+ *     partial sums) and its staging buffers, the same as one reference
+ *     kernel instance shares its command list (MNK:77-81).  Calls that use
+ *     them must not overlap: host-memory calls, products with M > 16, products
+ *     whose x is staged (fp32 x, x not 16-byte aligned, K not a multiple of
+ *     8) and M > 16 groups in stream-K order.  Issue those on one stream or
+ *     order them.  The other device-pointer calls (M <= 16 with 16-byte
+ *     aligned fp16 x and K a multiple of 8, mnb_group_run of M <= 16 groups
+ *     and of M > 16 groups in tile-list order) touch no shared buffer and may
+ *     run concurrently on distinct streams.
  *   - Pointers: by default x/y/out are DEVICE pointers and the call is
  *     asynchronous on `stream` (a hipStream_t; NULL = the context's stream).
  *     With MNB_HOST_MEMORY they are host pointers, the call copies through
@@ -205,11 +211,15 @@ int32_t mnb_supports_batch(const mnb_weight *w);
  * (MNK:2361, which is 256 there). */
 int32_t mnb_max_batch_rows(void);
 
-/* A recorded group of independent products executed as ONE launch.
- * Replaces recording several MatMulNBits dispatches into one command list
- * without barriers between them (recordInto / recordBatchDispatchOnly,
- * MNK:1935-2117; WarpExecutionContext.java:131-160; the batched layer
- * submissions of Phi3GpuPipeline.java:191-231): the items may run
+/* A recorded group of independent products executed as ONE launch.  No
+ * reference counterpart: the reference records every MatMulNBits dispatch
+ * into its command list with a UAV barrier after it (recordResidentInto /
+ * recordBatchDispatchOnly, MNK:1935-2117; WarpExecutionContext.java:131-160;
+ * the layer chain o_proj -> add -> rmsnorm -> gate_up -> swiglu -> down -> add
+ * of Phi3GpuPipeline.java:183-244).  That dependent form maps to
+ * stream-ordered device-pointer mnb_matmul calls (captured in a HIP graph to
+ * replay them); a group is for products that do not depend on each other
+ * (projections of one input, or of independent sequences): the items may run
  * concurrently, so no item may read another item's output.
  * Each item: device pointers, fp16 x [M, K] (K a multiple of 8, 16-byte
  * aligned), y [M, N] fp16 or fp32, M >= 1; all items share the weight variant
