@@ -197,6 +197,21 @@ int64_t mnb_weight_device_bytes(const mnb_weight *w);
 int32_t mnb_matmul(mnb_context *ctx, const mnb_weight *w, int32_t M, const void *x, int32_t x_type,
                    int64_t x_elems, void *y, int32_t y_type, int64_t y_elems, uint32_t flags, void *stream);
 
+/* mnb_matmul on device pointers that allocates nothing: no counterpart in
+ * the reference; for callers that cannot allocate device memory while they
+ * run (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, checks, kernels and results as mnb_matmul
+ * without MNB_HOST_MEMORY (which it refuses).  The GEMM's split-tile partial
+ * sums and the fp16 copy of x (made when x is fp32, not 16-byte aligned or K
+ * is not a multiple of 8) live in a fixed 80 MiB device array of the library
+ * instead of context buffers: 64 MiB of partial tiles and at most 16 MiB of
+ * staged x, M * roundup(K, 8) * 2 bytes (a larger staging need fails with
+ * MNB_ERR_INVALID_ARGUMENT).  Each GPU holds its own array for the life of
+ * the process; every call on one GPU shares it, so calls that overlap on one
+ * GPU (concurrent streams, other threads) race: order them. */
+int32_t mnb_matmul_noalloc(mnb_context *ctx, const mnb_weight *w, int32_t M, const void *x, int32_t x_type,
+                           int64_t x_elems, void *y, int32_t y_type, int64_t y_elems, uint32_t flags, void *stream);
+
 /* Dequantize to out[N, K] (K as passed at creation), w = (q - zp) * scale
  * computed in fp32 and written as fp32, or rounded to nearest-even fp16.
  * Replaces MatMulNBitsKernel.dequantizeInt4 (MNK:2674-2705); the fp32 output

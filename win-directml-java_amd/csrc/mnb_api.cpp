@@ -20,6 +20,7 @@
 
 #include "mnb_internal.h"
 
+using mnb::DeviceGuard;
 using mnb::WeightGeom;
 
 namespace {
@@ -127,18 +128,6 @@ bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
 size_t dtype_size(int32_t t) { return t == MNB_F32 ? 4 : 2; }
 
-struct DeviceGuard {
-    int prev = -1;
-    explicit DeviceGuard(int dev) {
-        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-        if (prev != dev) (void)hipSetDevice(dev);
-    }
-    ~DeviceGuard() {
-        int cur = -1;
-        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
-    }
-};
-
 }  // namespace
 
 int32_t mnb::report(int32_t code, const char *message) {
@@ -181,6 +170,14 @@ int32_t mnb_context_create(int32_t device, mnb_context **out) {
     // be captured into a HIP graph from the first call
     e = ensure(&c->sk_ws, &c->sk_ws_cap, mnb::sk_workspace_bytes(c->cu_count));
     if (e != hipSuccess) {
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return hip_fail(e, "init");
+    }
+    // the fixed scratch array of mnb_matmul_noalloc: its address on this device
+    e = mnb::noalloc_scratch(device, &c->scratch);
+    if (e != hipSuccess) {
+        (void)hipFree(c->sk_ws);
         (void)hipStreamDestroy(c->stream);
         delete c;
         return hip_fail(e, "init");
@@ -544,33 +541,35 @@ int32_t mnb_supports_batch(const mnb_weight *w) { return w ? 1 : 0; }
 
 int32_t mnb_max_batch_rows(void) { return std::numeric_limits<int32_t>::max() / 2; }
 
-// M > 16: stream-K GEMM over one persistent workgroup per CU.  The workspace
-// for the partial tiles of split tiles (sized for one workgroup per CU) lives
-// in the context and is allocated with it, so every call -- and graphs
-// captured from them -- uses the same buffer.  The kernel addresses x and the
-// weights with 32-bit byte offsets: rows of x go in chunks of at most 2 GiB,
-// and packed weights of 4 GiB or more are refused.
-static hipError_t launch_prefill(mnb_context *ctx, const mnb_weight *w, const mnb::MatmulArgs &a, hipStream_t s) {
+}  // extern "C"
+
+// M > 16: stream-K GEMM over one persistent workgroup per CU.  ws holds the
+// partial tiles of split tiles (sk_workspace_bytes(cu_count) bytes: the
+// context's workspace, allocated with it, or the fixed scratch array of
+// mnb_matmul_noalloc).  The kernel addresses x and the weights with 32-bit
+// byte offsets: rows of x go in chunks of at most 2 GiB, and packed weights of
+// 4 GiB or more are refused.
+static hipError_t launch_prefill(const mnb_weight *w, int cu_count, const mnb::MatmulArgs &a, float *ws,
+                                 hipStream_t s) {
     const mnb::WeightGeom &g = w->g;
     if ((uint64_t)g.NT * (uint64_t)g.ST * mnb::kTileBytes >= ((uint64_t)1 << 32)) return hipErrorInvalidValue;
     const int64_t chunk_rows = std::max<int64_t>(128, (((int64_t)1 << 31) / ((int64_t)a.ldx * 2)) / 128 * 128);
     const int chunk = (int)std::min<int64_t>(a.M, chunk_rows);
-    hipError_t e = ensure(&ctx->sk_ws, &ctx->sk_ws_cap, mnb::sk_workspace_bytes(ctx->cu_count));
-    if (e != hipSuccess) return e;
     const size_t y_row = (size_t)g.N * (a.y_type == MNB_F16 ? 2 : 4);
     for (int m0 = 0; m0 < a.M; m0 += chunk) {
         mnb::MatmulArgs c = a;
         c.M = std::min(chunk, a.M - m0);
         c.x = a.x + (size_t)m0 * a.ldx;
         c.y = (unsigned char *)a.y + (size_t)m0 * y_row;
-        const int G = mnb::sk_grid(mnb::sk_tiles(c.M, g.NT), g.ST, ctx->cu_count);
-        if ((e = mnb::launch_gemm_sk(w, c, G, (float *)ctx->sk_ws, s)) != hipSuccess) return e;
+        const int G = mnb::sk_grid(mnb::sk_tiles(c.M, g.NT), g.ST, cu_count);
+        const hipError_t e = mnb::launch_gemm_sk(w, c, G, ws, s);
+        if (e != hipSuccess) return e;
     }
     return hipSuccess;
 }
 
-int32_t mnb_matmul(mnb_context *ctx, const mnb_weight *w, int32_t M, const void *x, int32_t x_type, int64_t x_elems,
-                   void *y, int32_t y_type, int64_t y_elems, uint32_t flags, void *stream) {
+int32_t mnb::check_matmul(const mnb_context *ctx, const mnb_weight *w, int32_t M, const void *x, int32_t x_type,
+                          int64_t x_elems, const void *y, int32_t y_type, int64_t y_elems, uint32_t flags) {
     if (!ctx || !w) return fail(MNB_ERR_INVALID_STATE, "Kernel not prepared");
     if (w->ctx != ctx) return fail(MNB_ERR_INVALID_ARGUMENT, "weight belongs to another context");
     if (flags & ~(MNB_HOST_MEMORY | MNB_ACCUMULATE)) return fail(MNB_ERR_INVALID_ARGUMENT, "unknown flags 0x%x", flags);
@@ -584,41 +583,66 @@ int32_t mnb_matmul(mnb_context *ctx, const mnb_weight *w, int32_t M, const void 
         return fail(MNB_ERR_INVALID_ARGUMENT, "Input length %lld != K=%d", (long long)x_elems, g.K);
     if (x_elems < MK) return fail(MNB_ERR_INVALID_ARGUMENT, "xBatch too short: %lld < %lld", (long long)x_elems, (long long)MK);
     if (y_elems < MN) return fail(MNB_ERR_INVALID_ARGUMENT, "outBatch too short: %lld < %lld", (long long)y_elems, (long long)MN);
+    return MNB_OK;
+}
 
+size_t mnb::stage_x_bytes(const mnb_weight *w, int32_t M, const void *x, int32_t x_type) {
+    const WeightGeom &g = w->g;
+    if (x_type == MNB_F16 && (g.K % 8) == 0 && ((uintptr_t)x & 15u) == 0) return 0;
+    return (size_t)M * (size_t)((g.K + 7) & ~7) * 2;
+}
+
+hipError_t mnb::launch_product(const mnb_weight *w, int cu_count, int32_t M, const void *x, int32_t x_type, void *y,
+                               int32_t y_type, bool accumulate, void *stage_x, void *sk_ws, hipStream_t s) {
+    const WeightGeom &g = w->g;
+    const int32_t ldx_pad = (g.K + 7) & ~7;
+    mnb::MatmulArgs a;
+    a.x = (const _Float16 *)x;
+    a.ldx = g.K;
+    if (stage_x_bytes(w, M, x, x_type) != 0) {
+        const hipError_t e = mnb::launch_stage_x(x, x_type, M, g.K, ldx_pad, (_Float16 *)stage_x, s);
+        if (e != hipSuccess) return e;
+        a.x = (const _Float16 *)stage_x;
+        a.ldx = ldx_pad;
+    }
+    a.kx = ldx_pad;
+    a.M = M;
+    a.y = y;
+    a.y_type = y_type;
+    a.accumulate = accumulate ? 1 : 0;
+    return M <= mnb::kSkinnyMaxM ? mnb::launch_gemv(w, a, cu_count, s) : launch_prefill(w, cu_count, a, (float *)sk_ws, s);
+}
+
+extern "C" {
+
+int32_t mnb_matmul(mnb_context *ctx, const mnb_weight *w, int32_t M, const void *x, int32_t x_type, int64_t x_elems,
+                   void *y, int32_t y_type, int64_t y_elems, uint32_t flags, void *stream) {
+    const int32_t st = mnb::check_matmul(ctx, w, M, x, x_type, x_elems, y, y_type, y_elems, flags);
+    if (st != MNB_OK) return st;
+    const WeightGeom &g = w->g;
+    const int64_t MK = (int64_t)M * g.K, MN = (int64_t)M * g.N;
     const char *op = M == 1 ? "matvec" : "matmulBatch";
     DeviceGuard guard(ctx->device);
     hipStream_t s = (flags & MNB_HOST_MEMORY) || !stream ? ctx->stream : (hipStream_t)stream;
     const bool host = (flags & MNB_HOST_MEMORY) != 0;
-    const int32_t ldx_pad = (g.K + 7) & ~7;
     hipError_t e;
 
-    // activations: fp16 rows with a stride that is a multiple of 8 and 16-byte alignment
-    const _Float16 *xd = nullptr;
-    int32_t ldx = g.K;
-    const bool direct_ok = x_type == MNB_F16 && (g.K % 8) == 0;
+    // host arrays: x goes to a device staging buffer as it is (fp16 rows
+    // whose stride is a multiple of 8 land where the kernels read them)
+    const void *xd = x;
     if (host) {
-        if (direct_ok) {
-            if ((e = ensure(&ctx->stage_x, &ctx->stage_x_cap, (size_t)MK * 2)) != hipSuccess ||
-                (e = hipMemcpyAsync(ctx->stage_x, x, (size_t)MK * 2, hipMemcpyHostToDevice, s)) != hipSuccess)
-                return hip_fail(e, op);
-        } else {
-            if ((e = ensure(&ctx->stage_raw, &ctx->stage_raw_cap, (size_t)MK * dtype_size(x_type))) != hipSuccess ||
-                (e = ensure(&ctx->stage_x, &ctx->stage_x_cap, (size_t)M * ldx_pad * 2)) != hipSuccess ||
-                (e = hipMemcpyAsync(ctx->stage_raw, x, (size_t)MK * dtype_size(x_type), hipMemcpyHostToDevice, s)) != hipSuccess ||
-                (e = mnb::launch_stage_x(ctx->stage_raw, x_type, M, g.K, ldx_pad, (_Float16 *)ctx->stage_x, s)) != hipSuccess)
-                return hip_fail(e, op);
-            ldx = ldx_pad;
-        }
-        xd = (const _Float16 *)ctx->stage_x;
-    } else if (direct_ok && ((uintptr_t)x & 15u) == 0) {
-        xd = (const _Float16 *)x;
-    } else {
-        if ((e = ensure(&ctx->stage_x, &ctx->stage_x_cap, (size_t)M * ldx_pad * 2)) != hipSuccess ||
-            (e = mnb::launch_stage_x(x, x_type, M, g.K, ldx_pad, (_Float16 *)ctx->stage_x, s)) != hipSuccess)
+        void **buf = mnb::stage_x_bytes(w, M, ctx->stage_x, x_type) == 0 ? &ctx->stage_x : &ctx->stage_raw;
+        size_t *cap = buf == &ctx->stage_x ? &ctx->stage_x_cap : &ctx->stage_raw_cap;
+        const size_t bytes = (size_t)MK * dtype_size(x_type);
+        if ((e = ensure(buf, cap, bytes)) != hipSuccess ||
+            (e = hipMemcpyAsync(*buf, x, bytes, hipMemcpyHostToDevice, s)) != hipSuccess)
             return hip_fail(e, op);
-        xd = (const _Float16 *)ctx->stage_x;
-        ldx = ldx_pad;
+        xd = *buf;
     }
+    const size_t stage = mnb::stage_x_bytes(w, M, xd, x_type);
+    if (stage && (e = ensure(&ctx->stage_x, &ctx->stage_x_cap, stage)) != hipSuccess) return hip_fail(e, op);
+    if (M > mnb::kSkinnyMaxM && (e = ensure(&ctx->sk_ws, &ctx->sk_ws_cap, mnb::sk_workspace_bytes(ctx->cu_count))) != hipSuccess)
+        return hip_fail(e, op);
 
     void *yd = y;
     const size_t y_bytes = (size_t)MN * dtype_size(y_type);
@@ -630,15 +654,8 @@ int32_t mnb_matmul(mnb_context *ctx, const mnb_weight *w, int32_t M, const void 
             return hip_fail(e, op);
     }
 
-    mnb::MatmulArgs a;
-    a.x = xd;
-    a.ldx = ldx;
-    a.kx = ldx_pad;
-    a.M = M;
-    a.y = yd;
-    a.y_type = y_type;
-    a.accumulate = (flags & MNB_ACCUMULATE) ? 1 : 0;
-    e = M <= mnb::kSkinnyMaxM ? mnb::launch_gemv(w, a, ctx->cu_count, s) : launch_prefill(ctx, w, a, s);
+    e = mnb::launch_product(w, ctx->cu_count, M, xd, x_type, yd, y_type, (flags & MNB_ACCUMULATE) != 0, ctx->stage_x,
+                            ctx->sk_ws, s);
     if (e != hipSuccess) return hip_fail(e, op);
 
     if (host) {

@@ -71,6 +71,9 @@ struct mnb_context {
     // stream-K GEMM: fp32 partial tiles of split tiles
     void *sk_ws = nullptr;
     size_t sk_ws_cap = 0;
+    // device address of the fixed scratch array of mnb_matmul_noalloc on this
+    // context's device (shared by every context on the device)
+    void *scratch = nullptr;
     mnb_device_info info{};
 };
 
@@ -84,6 +87,23 @@ struct mnb_weight {
 };
 
 namespace mnb {
+
+// Makes `dev` the current device for the guard's lifetime.
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) (void)hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+// Device address of mnb_matmul_noalloc's fixed scratch array on `device`
+// (which must be current), looked up once per device (mnb_noalloc.hip).
+hipError_t noalloc_scratch(int device, void **out);
 
 // Kernel launchers (defined in the .hip files).  All take device pointers and
 // enqueue on `stream`; they return the launch status.
@@ -204,6 +224,20 @@ int sk_grid(int T, int ST, int cu_count);
 hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, hipStream_t stream);
 SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg, int ntw = kGemmNTW, int fm = kGemmFM);
 hipError_t launch_gemm_group(const GemmGroupPlan &g, float *ws, hipStream_t stream);
+
+// Argument checks of a product (the reference's messages); MNB_OK or the
+// status, with the message recorded.
+int32_t check_matmul(const mnb_context *ctx, const mnb_weight *w, int32_t M, const void *x, int32_t x_type,
+                     int64_t x_elems, const void *y, int32_t y_type, int64_t y_elems, uint32_t flags);
+// Bytes of staged fp16 x a product needs: 0 when x is 16-byte aligned fp16
+// and K is a multiple of 8 (the kernels read it in place), else M rows of K
+// rounded up to 8.
+size_t stage_x_bytes(const mnb_weight *w, int32_t M, const void *x, int32_t x_type);
+// One product on device pointers: x staged into stage_x when stage_x_bytes
+// says so, then the GEMV (M <= 16) or the GEMM, whose split tiles use
+// sk_ws (sk_workspace_bytes(cu_count) bytes).  Allocates nothing.
+hipError_t launch_product(const mnb_weight *w, int cu_count, int32_t M, const void *x, int32_t x_type, void *y,
+                          int32_t y_type, bool accumulate, void *stage_x, void *sk_ws, hipStream_t s);
 
 // largest M handled by the skinny (GEMV-style) kernel
 constexpr int kSkinnyMaxM = 16;

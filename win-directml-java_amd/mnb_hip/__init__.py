@@ -51,7 +51,7 @@ MNB_PACK_PHI3, MNB_PACK_QWEN2, MNB_PACK_ONNX = 1, 2, 3
 # Every symbol include/mnb.h declares.
 EXPORTED_SYMBOLS = (
     "mnb_version", "mnb_last_error", "mnb_context_create", "mnb_context_destroy", "mnb_context_info",
-    "mnb_weight_create", "mnb_weight_fuse_rows", "mnb_weight_quantize", "mnb_weight_read", "mnb_weight_destroy", "mnb_weight_shape", "mnb_weight_device_bytes", "mnb_matmul",
+    "mnb_weight_create", "mnb_weight_fuse_rows", "mnb_weight_quantize", "mnb_weight_read", "mnb_weight_destroy", "mnb_weight_shape", "mnb_weight_device_bytes", "mnb_matmul", "mnb_matmul_noalloc",
     "mnb_dequantize", "mnb_supports_batch", "mnb_max_batch_rows", "mnb_device_alloc", "mnb_device_free",
     "mnb_memcpy", "mnb_synchronize", "mnb_group_create", "mnb_group_run", "mnb_group_destroy",
     "mnb_pack_open", "mnb_pack_close", "mnb_pack_kind", "mnb_pack_weight_count", "mnb_pack_weight_name",
@@ -139,6 +139,7 @@ def load() -> ctypes.CDLL:
         "mnb_weight_shape": (i32, [vp, ctypes.POINTER(i32), ctypes.POINTER(i32), ctypes.POINTER(i32)]),
         "mnb_weight_device_bytes": (i64, [vp]),
         "mnb_matmul": (i32, [vp, vp, i32, vp, i32, i64, vp, i32, i64, u32, vp]),
+        "mnb_matmul_noalloc": (i32, [vp, vp, i32, vp, i32, i64, vp, i32, i64, u32, vp]),
         "mnb_dequantize": (i32, [vp, vp, vp, i32, i64, u32, vp]),
         "mnb_supports_batch": (i32, [vp]),
         "mnb_max_batch_rows": (i32, []),
