@@ -532,3 +532,50 @@ def test_mutated_files_fail_cleanly(tmp_path):
                     pass
             pk.close()
     assert opened > 0
+
+
+# ---------------------------------------------------------------------------
+# The reference's real Phi-3 export
+# ---------------------------------------------------------------------------
+
+PHI3_EXPORT = "/root/reference/model/phi3-mini-directml-int4/directml/directml-int4-awq-block-128/model.onnx"
+
+
+@pytest.mark.skipif(not os.path.exists(PHI3_EXPORT), reason="the reference checkout is not present")
+def test_reference_phi3_export_resolves_every_matmulnbits_triplet(tmp_path):
+    """The Phi-3-mini DirectML int4 AWQ export that the reference ships (its
+    external weights are a download, model.onnx.data.url): the graph beside a
+    sparse stand-in for model.onnx.data resolves 193 MatMulNBits triplets with
+    the shapes of Phi-3-mini (32 layers of q, k, v, o 3072 -> 3072, gate
+    3072 -> 16384 and down 8192 -> 3072, and the 3072 -> 32064 head), block
+    size 128, explicit zero points and fp16 scales, as Qwen2Weights'
+    MatMulNBits loading would (Q2W:534-545, 936-976); the layer lookup of
+    loadQuantizedProjection (Q2W:800-815) finds each projection."""
+    import collections
+    import shutil
+    model = tmp_path / "model.onnx"
+    shutil.copyfile(PHI3_EXPORT, model)
+    with open(tmp_path / "model.onnx.data", "wb") as f:
+        f.truncate(4 << 30)          # sparse: every tensor range lies inside, read as zeros
+    with Pack(str(model)) as pk:
+        assert pk.kind == mnb_hip.MNB_PACK_ONNX
+        names = pk.names()
+        assert len(names) == 193
+        shapes = collections.Counter()
+        for n in names:
+            i = pk.info(n)
+            assert i.block_size == 128 and i.zp_implicit == 0 and i.scale_dtype == 10, n
+            kb = i.K // 128
+            assert i.blocks_per_row == kb and i.q_bytes == i.N * kb * 64 and i.scale_count == i.N * kb, n
+            assert i.zp_bytes == (i.N * kb + 1) // 2, n
+            shapes[(i.K, i.N)] += 1
+        assert shapes == {(3072, 3072): 128, (3072, 16384): 32, (8192, 3072): 32, (3072, 32064): 1}
+        for layer in (0, 17, 31):
+            for proj in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "down_proj"):
+                name = pk.find_projection(layer, proj)
+                assert "layers.%d/" % layer in name and proj in name
+                K, N = (pk.info(name).K, pk.info(name).N)
+                assert (K, N) == {"down_proj": (8192, 3072), "gate_proj": (3072, 16384)}.get(proj, (3072, 3072))
+        assert pk.info("logits").N == 32064
+        q, s, z = pk.read(pk.find_projection(0, "q_proj"))
+        assert q.size == 3072 * 24 * 64 and s.size == 3072 * 24 and z.size == 3072 * 24 // 2
