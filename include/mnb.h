@@ -192,7 +192,10 @@ int64_t mnb_weight_device_bytes(const mnb_weight *w);
  *   y_elems         elements in y; must be >= M*N
  *   M               any M >= 1 (no 256-row chunking is needed)
  * Arithmetic: products of fp16 operands accumulated in fp32.  The output is
- * within 1e-3*sqrt(K)*max|x|*max|w| of the reference's fp32 CPU path.
+ * within 1e-3*sqrt(K)*max|x|*max|w| of the reference's fp32 CPU path, for any
+ * block scales (the device copy of a weight's scales carries a power of two
+ * that keeps every fp16 weight operand normal; results are scaled back
+ * exactly).  fp32 x is rounded to fp16 once, so |x| must stay below 65504.
  */
 int32_t mnb_matmul(mnb_context *ctx, const mnb_weight *w, int32_t M, const void *x, int32_t x_type,
                    int64_t x_elems, void *y, int32_t y_type, int64_t y_elems, uint32_t flags, void *stream);

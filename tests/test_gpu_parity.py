@@ -621,3 +621,97 @@ def test_group_of_prefill_products_accumulating_in_tile_list_order(ctx):
     assert sum(((M + 127) // 128) * ((N + 511) // 512) for M, K, N, _, _ in specs) == 1412
     for w, _, _ in _check_prefill_group(ctx, specs, 1900):
         w.close()
+
+
+# ------------------------------------------------ tiny scales, k tails ----
+
+def _tiny_scale_weight(seed, N, K, bs, lo, hi, zp):
+    """synth weight whose block scales are uniform in [lo, hi] (fp32, so not
+    rounded to fp16) with random signs."""
+    t = synth.make_weight(seed, N, K, bs, with_zp=zp)
+    rng = np.random.default_rng(seed + 1)
+    s = rng.uniform(lo, hi, t.N * t.kb).astype(np.float32) * rng.choice([-1.0, 1.0], t.N * t.kb).astype(np.float32)
+    return t, s
+
+
+def _oracle_f32_scales(t, s, x16):
+    kb = t.kb
+    zrp = t.zp_row_padded if t.zp_row_padded is not None else np.full((t.N, (kb + 1) // 2), 0x88, np.uint8)
+    z = synth.zp_row_padded_to_flat(zrp, t.N, kb)
+    kpad = kb * t.bs
+    x = np.zeros((x16.shape[0], kpad), np.float32)
+    x[:, : t.K] = x16.astype(np.float32)
+    y = orc.matmul(t.q, s, z, t.N, kpad, t.bs, x, threads=THREADS)
+    wmax = float(np.abs(orc.dequantize(t.q, s, z, t.N, kpad, t.bs)).max())
+    return y, wmax
+
+
+@pytest.mark.parametrize("lo,hi", [(1e-7, 1e-6), (2e-9, 3e-8), (1e-3, 4e-3)])
+def test_tiny_block_scales_keep_the_bound(ctx, lo, hi):
+    """Block scales far below fp16's normal range: products (q - zp) * s
+    below 6.1e-5 would be fp16 subnormals (absolute error up to 2^-25 each)
+    where a kernel folds the scale into its fp16 operand -- the GEMM at every
+    M > 16 and the bs = 16 GEMV.  Each weight keeps a power-of-two exponent
+    that lifts its largest |15 s| just below 65504 for that fold, undone
+    exactly on the fp32 sums, so all paths stay within the bound; fp32 and
+    subnormal fp16 scales, zero points or none, M = 1, 5, 40, 300, single
+    launches and groups, and the dequantization stays bit-exact."""
+    import torch
+    cases = [(700, 1000, 32, True), (300, 2048, 16, False), (513, 384, 64, True)]
+    for ci, (N, K, bs, zp) in enumerate(cases):
+        t, s = _tiny_scale_weight(8100 + ci, N, K, bs, lo, hi, zp)
+        zl = mnb_hip.MNB_ZP_ROW_PADDED if zp else None
+        w32 = mnb_hip.Weight(ctx, N, K, bs, t.q, s, t.zp_row_padded, zl)
+        s16 = s.astype(np.float16)          # fp16 scales: subnormal for most of these ranges
+        w16 = mnb_hip.Weight(ctx, N, K, bs, t.q, s16, t.zp_row_padded, zl)
+        try:
+            for w, sv, tag in ((w32, s, "f32"), (w16, s16.astype(np.float32), "f16")):
+                kb = t.kb
+                zrp = t.zp_row_padded if zp else np.full((N, (kb + 1) // 2), 0x88, np.uint8)
+                wd = w.dequantize(np.float32)
+                w_ref = orc.dequantize(t.q, sv, synth.zp_row_padded_to_flat(zrp, N, kb), N, kb * bs, bs)[:, :K]
+                assert np.array_equal(wd.view(np.uint32), np.ascontiguousarray(w_ref).view(np.uint32)), tag
+                for M in (1, 5, 40, 300):
+                    x16 = synth.make_x(8200 + M + ci, M, K)
+                    y_ref, wmax = _oracle_f32_scales(t, sv, x16)
+                    label = "tiny scales [%g, %g] %s N=%d K=%d bs=%d zp=%d M=%d" % (lo, hi, tag, N, K, bs, zp, M)
+                    assert_parity(w.matmul(x16, out_dtype=np.float32), y_ref, x16, t, wmax, False, label)
+                    if M > 1:     # one item of a group (the GEMM for M > 16, the 32-row GEMM or the GEMV group)
+                        xd = torch.from_numpy(x16).cuda()
+                        yd = torch.zeros((M, N), dtype=torch.float32, device="cuda")
+                        g = mnb_hip.Group(ctx, [(w, xd, yd)])
+                        torch.cuda.synchronize()     # the group runs on the context's stream
+                        g.run()
+                        torch.cuda.synchronize()
+                        g.close()
+                        assert_parity(yd.cpu().numpy(), y_ref, x16, t, wmax, False, label + " group")
+        finally:
+            w32.close()
+            w16.close()
+
+
+@pytest.mark.parametrize("K", [1001, 203, 4099])
+def test_single_products_with_a_k_tail_not_a_multiple_of_8(ctx, K):
+    """K % 8 != 0: the kernels read x in 16-byte pieces, so x is first copied
+    to fp16 rows padded to a multiple of 8 with zeros (host arrays, and device
+    fp16 or fp32 x alike); M = 1, 7 (GEMV) and 40, 200 (GEMM, split tiles),
+    zero points, bs 32 and 64."""
+    import torch
+    for bs in (32, 64):
+        t = synth.make_weight(8300 + K + bs, 300, K, bs, with_zp=True)
+        w = upload(ctx, t)
+        try:
+            for M in (1, 7, 40, 200):
+                x16 = synth.make_x(8400 + M + K, M, K)
+                y_ref, wmax = oracle_matmul(t, x16)
+                label = "k tail K=%d bs=%d M=%d" % (K, bs, M)
+                assert_parity(w.matmul(x16, out_dtype=np.float16), y_ref, x16, t, wmax, True, label + " host f16")
+                for xdt in (torch.float16, torch.float32):
+                    xd = torch.from_numpy(x16).cuda().to(xdt)
+                    yd = torch.empty((M, 300), dtype=torch.float32, device="cuda")
+                    torch.cuda.synchronize()
+                    w.matmul(xd, yd)
+                    torch.cuda.synchronize()
+                    assert_parity(yd.cpu().numpy(), y_ref, x16, t, wmax, False, label + " device %s" % xdt)
+        finally:
+            w.close()

@@ -9,6 +9,7 @@
 // of the reference are replaced by one HIP stream per context.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -129,6 +130,13 @@ bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 size_t dtype_size(int32_t t) { return t == MNB_F32 ? 4 : 2; }
 
 }  // namespace
+
+int32_t mnb::fold_exponent(double max_abs_scale) {
+    if (!(max_abs_scale > 0.0) || !std::isfinite(max_abs_scale)) return 0;
+    int32_t e = 0;
+    while (e < 100 && std::ldexp(15.0 * max_abs_scale, e + 1) <= 65504.0) ++e;
+    return e;
+}
 
 int32_t mnb::report(int32_t code, const char *message) {
     g_last_error = message ? message : "";
@@ -301,6 +309,15 @@ int32_t mnb_weight_create(mnb_context *ctx, int32_t N, int32_t K, int32_t block_
             s16.clear();
         }
     }
+    // the power of two the device copy of the scales carries (see mnb_internal.h)
+    double max_abs_scale = 0.0;
+    for (int64_t i = 0; i < blocks; ++i) {
+        const double v = scale_type == MNB_F32 ? (double)((const float *)scales)[i]
+                                               : (double)f16_bits_to_f32(((const uint16_t *)scales)[i]);
+        if (std::fabs(v) > max_abs_scale || std::isnan(v)) max_abs_scale = std::isnan(v) ? NAN : std::fabs(v);
+        if (std::isnan(max_abs_scale)) break;
+    }
+    g.fold_exp = mnb::fold_exponent(max_abs_scale);
 
     DeviceGuard guard(ctx->device);
     mnb_weight *w = new mnb_weight();
@@ -372,6 +389,10 @@ int32_t mnb_weight_fuse_rows(mnb_context *ctx, const mnb_weight *const *parts, i
     WeightGeom g = mnb::make_geom((int32_t)rows, parts[0]->g.K, parts[0]->g.bs);
     g.scale_f32 = any_f32 ? 1 : 0;
     g.has_zp = any_zp ? 1 : 0;
+    // the smallest exponent of the parts: every part's stored scales move
+    // toward the caller's values, so none can overflow
+    g.fold_exp = parts[0]->g.fold_exp;
+    for (int32_t i = 1; i < count; ++i) g.fold_exp = std::min(g.fold_exp, parts[i]->g.fold_exp);
 
     DeviceGuard guard(ctx->device);
     mnb_weight *w = new mnb_weight();
@@ -473,6 +494,26 @@ int32_t mnb_weight_quantize(mnb_context *ctx, const void *data, int32_t data_typ
         return hip_fail(e, "prepare");
     }
     if (staged) (void)hipFree(staged);
+    // the scales' power of two (see mnb_internal.h), from the quantized scales
+    {
+        std::vector<float> sh(s_t_bytes / 4);
+        if ((e = hipMemcpy(sh.data(), w->s_t, s_t_bytes, hipMemcpyDeviceToHost)) == hipSuccess) {
+            double max_abs_scale = 0.0;
+            for (float v : sh) max_abs_scale = std::max(max_abs_scale, (double)std::fabs(v));
+            w->g.fold_exp = mnb::fold_exponent(max_abs_scale);
+            if (w->g.fold_exp != 0 &&
+                (e = mnb::launch_scale_f32((float *)w->s_t, sh.size(), mnb::pow2f(w->g.fold_exp), ctx->stream)) ==
+                    hipSuccess)
+                e = hipStreamSynchronize(ctx->stream);
+        }
+        if (e != hipSuccess) {
+            (void)hipFree(w->q_t);
+            (void)hipFree(w->s_t);
+            (void)hipFree(w->zp_t);
+            delete w;
+            return hip_fail(e, "prepare");
+        }
+    }
     w->bytes = (int64_t)(q_t_bytes + s_t_bytes + z_t_bytes);
     ctx->live_weights++;
     *out = w;
@@ -897,6 +938,7 @@ int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *
         p.y = it.y;
         p.y_f16 = it.y_type == MNB_F16;
         p.accumulate = (it.flags & MNB_ACCUMULATE) ? 1 : 0;
+        p.unfold = mnb::pow2f(-g.fold_exp);
         host[(size_t)i].first_wg = (int32_t)wgs;
         wgs += g.NT;
         const int stw = m1 ? 4 : mnb::kGemvRowsSTW;

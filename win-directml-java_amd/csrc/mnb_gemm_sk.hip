@@ -435,6 +435,13 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     // Fragment (a, f), register v of lane (c32, h): row a * 32 + c32 of the
     // tile, column 32 f + 8 (v / 4) + 4 h + v % 4 of the wave's 32 columns.
     auto epilogue = [&](int nst) __attribute__((always_inline)) {
+        // undo the stored scales' 2^fold_exp (exact), for whole and partial tiles alike
+#pragma unroll
+        for (int a = 0; a < FM; ++a)
+#pragma unroll
+            for (int f = 0; f < FN; ++f)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[a][f][v] *= ic.unfold;
         const int m0 = (t % ic.MT) * BM, ng = t / ic.MT;
         const int c_wave = wave * NTW * kTileRows;   // first column of this wave in the tile
         if (nst == ic.ST) {
@@ -848,6 +855,7 @@ SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg, int 
     it.y_f16 = a.y_type == MNB_F16;
     it.accumulate = a.accumulate;
     it.y_vec = (g.N % 4 == 0) && ((uintptr_t)a.y % (it.y_f16 ? 8 : 16) == 0);
+    it.unfold = pow2f(-g.fold_exp);
     it.ibeg = ibeg;
     return it;
 }

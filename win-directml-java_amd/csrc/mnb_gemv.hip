@@ -199,6 +199,11 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
         }
     }
 
+    // undo the stored scales' factor 2^fold_exp (exact)
+    acc[0] *= p.unfold;
+    acc[1] *= p.unfold;
+    acc[2] *= p.unfold;
+    acc[3] *= p.unfold;
     // D layout of the 16x16 MFMA result: lane (gg*16 + r) holds rows 4*gg+i, column r.
     const int n = nt * kTileRows + r;
     if (n >= p.N) return;
@@ -310,6 +315,7 @@ hipError_t launch_gemv(const mnb_weight *w, const MatmulArgs &a, int32_t cu_coun
     p.y = a.y;
     p.y_f16 = a.y_type == MNB_F16;
     p.accumulate = a.accumulate;
+    p.unfold = pow2f(-g.fold_exp);
     GemvLaunch L;
     const bool m1 = a.M == 1;
     L.stw = gemv_stw_for(g, cu_count > 0 ? cu_count : 256, m1);

@@ -22,6 +22,13 @@
 //   Scales: [NT][ST][16][SPS] of fp16 (or fp32 when the caller's fp32 scales
 //   are not all fp16-exact), SPS = max(1, 128/bs) scales per row per
 //   super-tile; entry i is the scale of block (st*128)/bs + i.
+//   The stored scales are the caller's times 2^fold_exp (fold_exp >= 0, per
+//   weight, chosen so that 15 * max|scale| * 2^fold_exp <= 65504): where a
+//   kernel folds the scale into an fp16 weight operand, (q - zp) * scale *
+//   2^fold_exp stays in fp16's normal range however small the scales are, and
+//   every consumer multiplies its fp32 result by 2^-fold_exp (exact, so
+//   results are those of the unscaled scales wherever the unscaled fp16 fold
+//   would not have been subnormal).
 //   Zero points (optional): [NT][ST][16] entries of ZB = max(1, SPS/2) bytes,
 //   nibble i (low nibble first) belongs to the same block as scale i.
 //   Rows >= N, blocks >= kb and k >= kb*bs are stored as zero nibbles, zero
@@ -50,9 +57,17 @@ struct WeightGeom {
     int32_t SPS = 0, ZB = 0;      // scales per row per super-tile, zp bytes per row per super-tile
     int32_t scale_f32 = 0;        // 1: device scales are fp32
     int32_t has_zp = 0;           // 0: implicit zero point 8
+    int32_t fold_exp = 0;         // stored scales = scales * 2^fold_exp
 };
 
 WeightGeom make_geom(int32_t N, int32_t K, int32_t bs);
+
+// 2^e as a float, -126 <= e <= 127 (exact).
+__host__ __device__ inline float pow2f(int e) { return __builtin_bit_cast(float, (uint32_t)(e + 127) << 23); }
+
+// The largest e in [0, 100] with 15 * max_abs_scale * 2^e <= 65504 (0 for a
+// zero, infinite or NaN maximum).
+int32_t fold_exponent(double max_abs_scale);
 
 }  // namespace mnb
 
@@ -117,11 +132,16 @@ hipError_t launch_repack(const WeightGeom &g, const uint8_t *q_nat, const void *
 
 // Copies the N_src rows of one tiled weight into rows [row0, row0 + N_src) of
 // another with the same K and block size (row fusion).  dst must be zero
-// beforehand.  Scales widen fp16 -> fp32 when dst keeps fp32 scales; a source
+// beforehand.  Scales widen fp16 -> fp32 when dst keeps fp32 scales and are
+// multiplied by 2^(dst fold_exp - src fold_exp) (dst's exponent is at most
+// src's, so the stored value only moves toward the caller's); a source
 // without zero points writes zero point 8 for its blocks < kb.
 hipError_t launch_copy_rows(const WeightGeom &src_g, const void *src_q, const void *src_s, const void *src_zp,
                             const WeightGeom &dst_g, void *dst_q, void *dst_s, void *dst_zp, int32_t row0,
                             hipStream_t stream);
+
+// s[i] *= factor for the n tiled fp32 scales of a weight (a power of two).
+hipError_t launch_scale_f32(float *s, size_t n, float factor, hipStream_t stream);
 
 // data[N, K] (f32 or f16, row stride K, K a multiple of g.bs, g.bs in
 // {16, 32, 64, 128}) -> tiled weight with fp32 scales and zero points: the
@@ -161,6 +181,7 @@ struct GemvParams {
     int32_t ldx, kx, M, N, ST;
     void *y;
     int32_t y_f16, accumulate;
+    float unfold;     // 2^-fold_exp of the weight
 };
 
 // One item of a group launch (device-resident array).

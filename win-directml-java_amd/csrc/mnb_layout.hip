@@ -67,6 +67,18 @@ __global__ void repack_q_kernel(WeightGeom g, const uint8_t *__restrict__ q_nat,
     *(u32x4_t *)(q_t + c * 4) = out;
 }
 
+// s * 2^e rounded to the scale type (exact: the product stays within the
+// type's finite range by the choice of the exponents).  The fp32 product is
+// kept in a register first: fused into one mixed-precision multiply-add with a
+// +0 addend, a -0 scale would come out as +0.
+template <typename ScaleT, typename SrcT>
+__device__ __forceinline__ ScaleT scaled(SrcT s, float factor) {
+    float f = (float)s * factor;
+    asm volatile("" : "+v"(f));
+    return (ScaleT)f;
+}
+
+// Scales in tile order, times 2^fold_exp.
 template <typename ScaleT>
 __global__ void repack_scales_kernel(WeightGeom g, const ScaleT *__restrict__ s_nat, ScaleT *__restrict__ s_t) {
     const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -81,7 +93,7 @@ __global__ void repack_scales_kernel(WeightGeom g, const ScaleT *__restrict__ s_
     const int n = nt * kTileRows + r;
     const int blk = g.bs >= kTileK ? (st * kTileK) / g.bs : st * g.SPS + i;
     ScaleT v = (ScaleT)0;
-    if (n < g.N && blk < g.kb) v = s_nat[(size_t)n * g.kb + blk];
+    if (n < g.N && blk < g.kb) v = scaled<ScaleT>(s_nat[(size_t)n * g.kb + blk], pow2f(g.fold_exp));
     s_t[e] = v;
 }
 
@@ -153,8 +165,9 @@ __global__ void copy_rows_kernel(WeightGeom sg, const uint32_t *__restrict__ sq,
 #pragma unroll
     for (int gg = 0; gg < 4; ++gg)
         *(u32x4_t *)(dq + (td * 64 + gg * 16 + ld) * 4) = *(const u32x4_t *)(sq + (ts * 64 + gg * 16 + ls) * 4);
+    const float factor = pow2f(dg.fold_exp - sg.fold_exp);
     for (int i = 0; i < sg.SPS; ++i)
-        ds[(td * kTileRows + ld) * dg.SPS + i] = (DstS)ss[(ts * kTileRows + ls) * sg.SPS + i];
+        ds[(td * kTileRows + ld) * dg.SPS + i] = scaled<DstS>(ss[(ts * kTileRows + ls) * sg.SPS + i], factor);
     if (!dz) return;
     if (sz) {
         for (int b = 0; b < sg.ZB; ++b) dz[(td * kTileRows + ld) * dg.ZB + b] = sz[(ts * kTileRows + ls) * sg.ZB + b];
@@ -189,6 +202,18 @@ hipError_t launch_copy_rows(const WeightGeom &sg, const void *sq, const void *ss
     return hipGetLastError();
 }
 
+__global__ void scale_f32_kernel(float *__restrict__ s, size_t n, float factor) {
+    const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e < n) s[e] *= factor;
+}
+
+hipError_t launch_scale_f32(float *s, size_t n, float factor, hipStream_t stream) {
+    const unsigned T = 256;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(scale_f32_kernel, dim3(blocks_for(n, T)), dim3(T), 0, stream, s, n, factor);
+    return hipGetLastError();
+}
+
 template <typename XT>
 __global__ void stage_x_kernel(const XT *__restrict__ x, int32_t M, int32_t K, int32_t ldx, _Float16 *__restrict__ out) {
     const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -212,7 +237,9 @@ hipError_t launch_stage_x(const void *x, int32_t x_type, int32_t M, int32_t K, i
     return hipGetLastError();
 }
 
-// One thread per (row n, group of 8 consecutive k).  w = float(q - zp) * scale.
+// One thread per (row n, group of 8 consecutive k).  w = float(q - zp) * scale,
+// formed as (float(q - zp) * stored scale) * 2^-fold_exp: the power of two
+// makes the two roundings one.
 template <typename ScaleT, typename OutT, bool HAS_ZP>
 __global__ void dequant_kernel(WeightGeom g, const uint32_t *__restrict__ q_t, const ScaleT *__restrict__ s_t,
                                const uint8_t *__restrict__ zp_t, OutT *__restrict__ out) {
@@ -229,6 +256,7 @@ __global__ void dequant_kernel(WeightGeom g, const uint32_t *__restrict__ q_t, c
     const uint32_t t = q_t[(tile * 64 + gg * 16 + r) * 4 + j];
     const int si = g.bs >= kTileK ? 0 : kk / g.bs;
     const float scale = (float)s_t[(tile * kTileRows + r) * g.SPS + si];
+    const float unfold = pow2f(-g.fold_exp);
     int z = 8;
     if constexpr (HAS_ZP) {
         const uint8_t *zp = zp_t + (tile * kTileRows + r) * g.ZB;
@@ -239,7 +267,7 @@ __global__ void dequant_kernel(WeightGeom g, const uint32_t *__restrict__ q_t, c
     for (int i = 0; i < 8; ++i) {
         if (k0 + i < g.K) {
             const int w = (int)tiled_nibble(t, i) - z;
-            float v = (float)w * scale;
+            float v = (float)w * scale * unfold;
             // Keep the binary32 product in a register before the fp16 rounding:
             // otherwise the multiply and the conversion are fused into
             // v_fma_mix(scale, w, +0), which turns a -0 product into +0.

@@ -249,7 +249,7 @@ __global__ void unpack_scales_zp_kernel(WeightGeom g, const ScaleT *__restrict__
         const int blk = g.bs >= kTileK ? (st * kTileK) / g.bs : st * g.SPS + i;
         if (blk >= g.kb) continue;
         if (g.bs > kTileK && st * kTileK != blk * g.bs) continue;
-        s_nat[(size_t)n * g.kb + blk] = (float)s_t[e * g.SPS + i];
+        s_nat[(size_t)n * g.kb + blk] = (float)s_t[e * g.SPS + i] * pow2f(-g.fold_exp);
         zp_blocks[(size_t)n * g.kb + blk] = zp_t ? (uint8_t)((bits >> (4 * i)) & 0xFu) : (uint8_t)8;
     }
 }

@@ -20,6 +20,7 @@ struct SkItem {
     int32_t NT, ST, MT, T;      // n-tiles, super-tiles (stages), m-tiles, output tiles
     int32_t y_f16, accumulate;
     int32_t y_vec;              // N % 4 == 0 and y aligned for 4-element stores
+    float unfold;               // 2^-fold_exp of the weight: undoes its stored scale factor
     int32_t ibeg;
 };
 

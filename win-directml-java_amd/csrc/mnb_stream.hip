@@ -29,6 +29,7 @@ struct UnitRef {
     const _Float16 *x;     // activation row
     void *y;
     int32_t ST, kx, N, nt, y_f16, accumulate;
+    float unfold;
 };
 
 template <typename ScaleT, int SPS, int ZB>
@@ -50,6 +51,7 @@ __device__ __forceinline__ UnitRef<ScaleT> resolve_unit(const GroupItem *__restr
     u.nt = nt;
     u.y_f16 = p.y_f16;
     u.accumulate = p.accumulate;
+    u.unfold = p.unfold;
     return u;
 }
 
@@ -140,8 +142,9 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
             // x was broadcast to all 16 MFMA rows: lanes 0..15 hold row 0, column r
             const int n = cref.nt * kTileRows + r;
             if (gg == 0 && n < cref.N) {
-                if (cref.y_f16) store_y<true>(cref.y, (size_t)n, acc, cref.accumulate != 0);
-                else store_y<false>(cref.y, (size_t)n, acc, cref.accumulate != 0);
+                const float v = acc * cref.unfold;   // undo the stored scales' 2^fold_exp
+                if (cref.y_f16) store_y<true>(cref.y, (size_t)n, v, cref.accumulate != 0);
+                else store_y<false>(cref.y, (size_t)n, v, cref.accumulate != 0);
             }
             acc = 0.f;
             cst = 0;
