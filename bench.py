@@ -60,14 +60,16 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--settle-ms", type=float, default=SETTLE_MS,
                    help="untimed GPU work before the warm-up steps of each timed phase (clock ramp after idle)")
-    p.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="bounded CPU-baseline sample (M=1)")
+    p.add_argument("--cpu-m512-seconds", type=float, default=15.0, help="bounded CPU-baseline sample (M=512)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-sweep", action="store_true")
     p.add_argument("--eager", action="store_true", help="launch directly instead of via HIP graphs (counter runs)")
-    p.add_argument("--phase", choices=("all", "decode", "prefill", "qwen", "config0"), default="all",
-                   help="decode: only the M=1 group launch and the copy calibration; prefill: only the "
-                        "M=512 launches (both for counter runs); qwen: only the Qwen2.5-0.5B step at M=1 and 64; "
-                        "config0: only the single qkv product at M=1")
+    p.add_argument("--phase", choices=("all", "decode", "chain", "prefill", "qwen", "config0"), default="all",
+                   help="decode: only the M=1 group launch and the copy calibration; chain: only the 129 M=1 "
+                        "launches in stream order (a HIP graph); prefill: only the M=512 launches (both for "
+                        "counter runs); qwen: only the Qwen2.5-0.5B step at M=1 and 64; config0: only the single "
+                        "qkv product at M=1")
     p.add_argument("--prefill-group", action="store_true",
                    help="with --phase prefill: the 129 projections as one group launch instead of 129 launches")
     p.add_argument("--prefill-m", type=int, default=512, help="with --phase prefill: rows M of the prefill step")
@@ -215,8 +217,20 @@ def measured_traffic(kernel_profile, key="traffic_bytes_per_launch"):
     return None
 
 
-def cpu_baseline(host, projs, seconds):
-    """Oracle restatement of the reference CPU path on a bounded sample."""
+def cpu_baseline(host, projs, seconds, m512_seconds):
+    """Oracle restatement of the reference CPU path on bounded samples.
+
+    M = 1: decode-step projections in step order for about `seconds` (GB/s of
+    algorithmic bytes, the headline unit).  M = 512: one projection of each
+    Phi-3 shape (qkv, o_proj, gate_up, down, lm_head) with 512 fp32 activation
+    rows through the reference's matmul loop (QuantizedWeight.matmul,
+    Phi3Weights.java:157-192, which dequantizes every block again for each
+    row), TFLOP/s over those five; a shape whose estimated time would pass
+    `m512_seconds` in total runs on a prefix of its rows instead (the rate is
+    per row).  Threads: one per core the process may use, at most 16.  No JDK
+    is probed for beyond PATH: with one, the reference's own Java path could
+    be timed; without, the C restatement is (kind "port")."""
+    import shutil
     import mnb_oracle as orc
     threads = max(1, min(16, len(os.sched_getaffinity(0))))
     orc.build()
@@ -235,10 +249,38 @@ def cpu_baseline(host, projs, seconds):
         t_total += time.perf_counter() - t0
         done_bytes += t.algorithmic_bytes(1)
         done += 1
+    # M = 512: one projection per shape, rows capped by the time budget
+    shapes, flops, secs, rows_done = {}, 0.0, 0.0, {}
+    for (name, layer, K, N), t in zip(projs, host):
+        if name not in shapes:
+            shapes[name] = t
+    rate = None     # flop/s measured so far, to size the later shapes
+    for name, t in shapes.items():
+        M = 512
+        if rate is not None:
+            left = max(0.5, m512_seconds - secs) / max(1, len(shapes) - len(rows_done))
+            M = max(8, min(512, int(left * rate / (2.0 * t.N * t.K))))
+        s32 = orc.fp16_bits_to_fp32(t.scales_f16.view(np.uint16))
+        z = np.full((t.N * t.kb + 1) // 2, 0x88, np.uint8)
+        x = rng.standard_normal((M, t.K)).astype(np.float16).astype(np.float32)
+        t0 = time.perf_counter()
+        orc.matmul(t.q, s32, z, t.N, t.K, BLOCK, x, lanes=8, threads=threads)
+        dt = time.perf_counter() - t0
+        secs += dt
+        flops += 2.0 * M * t.N * t.K
+        rate = flops / secs
+        rows_done[name] = M
+    jdk = shutil.which("java")
     return {"value": round(done_bytes / t_total / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "host_cpus": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)), "jdk": jdk,
             "sample": "%d decode-step projections at M=1 in step order (%.2f GB of weights, %.2f steps), fp32 "
                       "activations, 8-lane FMA block dot, %d threads, %.1f s" % (
-                          done, done_bytes / 1e9, done / len(projs), threads, t_total)}
+                          done, done_bytes / 1e9, done / len(projs), threads, t_total),
+            "m512": {"value": round(flops / secs / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+                     "rows": rows_done, "seconds": round(secs, 2),
+                     "sample": "one projection per Phi-3 shape with 512 fp32 activation rows (fewer where the "
+                               "time budget ran out: rows listed), the reference's matmul loop that dequantizes "
+                               "every block again per row, 8-lane FMA block dot, %d threads" % threads}}
 
 
 def qwen_tied_lm_head(torch, mnb_hip, ctx, stream, args):
@@ -463,6 +505,19 @@ def main():
     xs = [torch.randn(K, device="cuda", generator=gen).half() for (_, _, K, _) in projs]
     ys = [torch.empty(N, device="cuda", dtype=torch.float16) for (_, _, _, N) in projs]
 
+    if args.phase == "chain":
+        dec = Launcher(ctx, weights, xs, ys, 1, stream)
+        g_dec = capture(torch, dec, stream)
+        wall_seq, gpu_seq = time_graph(torch, g_dec, stream, args.steps, args.warmup, args.settle_ms)
+        print(json.dumps({"phase": "chain", "gbs": round(bytes_step / wall_seq / 1e9, 2),
+                          "us_per_step": round(wall_seq * 1e6, 2), "gpu_us_per_step": round(gpu_seq * 1e6, 2),
+                          "launches_per_step": len(projs), "bytes_per_step": bytes_step}), flush=True)
+        del g_dec
+        for w in weights:
+            w.close()
+        ctx.close()
+        return
+
     # (1) headline: the 129 projections (each with its own activation, no
     #     dependence between them) recorded once as a group and run as one
     #     launch of the streaming kernel.
@@ -560,7 +615,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(host, projs, args.cpu_seconds)
+        cpu = cpu_baseline(host, projs, args.cpu_seconds, args.cpu_m512_seconds)
         log("cpu baseline: %s" % json.dumps(cpu))
 
     result = {
