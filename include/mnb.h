@@ -267,6 +267,29 @@ int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *
 int32_t mnb_group_run(mnb_context *ctx, const mnb_group *group, void *stream);
 int32_t mnb_group_destroy(mnb_group *group);
 
+/* Which kernel and work order a product or a recorded group runs (no
+ * reference counterpart: the schedule is chosen by cost models, and this
+ * lets callers and tests see the choice). */
+#define MNB_KERNEL_GEMV 1        /* one workgroup per 16-row n-tile, waves split K (M <= 16) */
+#define MNB_KERNEL_STREAM 2      /* persistent weight stream over (product, n-tile) units (M == 1 groups) */
+#define MNB_KERNEL_GEMV_GROUP 3  /* the GEMV kernel over every product's n-tiles (1 < M <= 16 groups) */
+#define MNB_KERNEL_GEMM 4        /* the MFMA GEMM */
+#define MNB_ORDER_NONE 0         /* one unit of work per workgroup or a static unit list */
+#define MNB_ORDER_STREAM_K 1     /* (tile, k-stage) iterations cut into equal ranges; split tiles reduced after */
+#define MNB_ORDER_TILE_LIST 2    /* whole tiles per workgroup from a tile list (a table, or closed form for one product) */
+typedef struct mnb_plan_info {
+    int32_t kernel;      /* MNB_KERNEL_* */
+    int32_t order;       /* MNB_ORDER_* */
+    int32_t tile_rows;   /* GEMM output tile: rows of x (32, 64 or 128); 0 otherwise */
+    int32_t tile_cols;   /* GEMM output tile: columns (256 or 512); 16 for the GEMV kernels */
+    int32_t workgroups;  /* grid size */
+} mnb_plan_info;
+/* The plan of mnb_matmul(ctx, w, M, ...) with device pointers (for M
+ * beyond 2 GiB of x rows, the plan of the first chunk of rows). */
+int32_t mnb_matmul_plan(const mnb_context *ctx, const mnb_weight *w, int32_t M, mnb_plan_info *out);
+/* The plan recorded by mnb_group_create. */
+int32_t mnb_group_plan(const mnb_group *group, mnb_plan_info *out);
+
 /* Device buffers for resident activations (WarpGpuBuffer in the reference,
  * used by MNK:1687-1832). */
 int32_t mnb_device_alloc(mnb_context *ctx, int64_t bytes, void **out);

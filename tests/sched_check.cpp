@@ -2,7 +2,9 @@
 //   tile list of a grouped prefill GEMM (mnb::sk_tile_list): G, then one line
 //     "MT NG ST" per item;
 //   streaming M = 1 schedule (mnb::stream_schedule): the word "stream", the
-//     wave count, then one line "NT ST" per item.
+//     wave count, then one line "NT ST" per item;
+//   closed-form tile list of a single item (mnb::sk_cf_*): the word "closed",
+//     then lines "G MT NG ST", each checked against sk_tile_list of that item.
 // Exits 1 on the first broken invariant; prints balance (and, for the tile
 // list, locality) figures.
 #include <stdio.h>
@@ -77,10 +79,43 @@ static int check_stream() {
     return 0;
 }
 
+// The closed form must give every workgroup exactly the tiles, in the same
+// order, and the same first iteration as the table sk_tile_list builds for
+// the same single item.
+static int check_closed() {
+    int G, MT, NG, ST, cases = 0;
+    while (scanf("%d %d %d %d", &G, &MT, &NG, &ST) == 4) {
+        std::vector<SkItem> items(1);
+        SkItem &it = items[0];
+        it = SkItem{};
+        it.MT = MT;
+        it.T = MT * NG;
+        it.ST = ST;
+        std::vector<SkTile> seq;
+        std::vector<SkRange> wg;
+        sk_tile_list(items, G, seq, wg);
+        for (int g = 0; g <= G; ++g) {
+            const int first = sk_cf_first(it.T, G, g);
+            if (wg[(size_t)g].pos != first || wg[(size_t)g].iter != first * ST) return fail("workgroup start", g, first);
+            if (g == G) break;
+            const int n = sk_cf_first(it.T, G, g + 1) - first;
+            for (int j = 0; j < n; ++j) {
+                const int t = sk_cf_tile(MT, NG, sk_cf_base(it.T, G, g) + j * sk_cf_step(G));
+                if (seq[(size_t)(first + j)].t != t || seq[(size_t)(first + j)].item != 0)
+                    return fail("tile", g * 100000L + j, t);
+            }
+        }
+        ++cases;
+    }
+    printf("ok closed cases=%d\n", cases);
+    return 0;
+}
+
 int main() {
     char first[32] = {0};
     if (scanf("%31s", first) != 1) return fail("input", 0, 0);
     if (strcmp(first, "stream") == 0) return check_stream();
+    if (strcmp(first, "closed") == 0) return check_closed();
     const int G = atoi(first);
     if (G < 1) return fail("input", G, 0);
     std::vector<SkItem> items;

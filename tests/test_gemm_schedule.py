@@ -124,3 +124,30 @@ def test_stream_schedule_random_groups(checker, seed):
     waves = int(rng.choice([1, 7, 64, 1024, 3072]))
     items = [(int(rng.integers(1, 3000)), int(rng.integers(1, 80))) for _ in range(int(rng.integers(1, 60)))]
     run_stream(checker, waves, items)
+
+
+# ------------------------------------------- single items in closed form
+
+def test_closed_form_equals_the_table_of_a_single_item(checker):
+    """A single product runs in tile-list order without a device table: the
+    kernel computes its workgroup's tiles from the tile count (mnb::sk_cf_*).
+    For every grid and shape here the closed form gives each workgroup the
+    same tiles, in the same order, as sk_tile_list builds for that item: the
+    Phi-3 and Qwen products at M in {16, 64, 128, 512, 2048} with 128-, 64-
+    and 32-row and 256- and 512-column tiles, and random shapes and grids
+    (grids not a multiple of 8, fewer tiles than workgroups, one m-tile,
+    ragged m-chunks of 1 to 3 m-tiles)."""
+    rng = np.random.default_rng(7)
+    lines = []
+    for M in (16, 64, 128, 512, 2048):
+        for K, N in [(3072, 9216), (3072, 3072), (3072, 16384), (8192, 3072), (3072, 32064), (896, 1152),
+                     (4864, 896), (896, 151936)]:
+            for bm, bn in ((128, 256), (128, 512), (64, 512), (32, 512)):
+                MT, NG, ST = -(-M // bm), -(-N // bn), -(-K // 128)
+                for G in (256, 248, min(256, MT * NG)):
+                    lines.append("%d %d %d %d" % (G, MT, NG, ST))
+    for _ in range(400):
+        lines.append("%d %d %d %d" % (int(rng.integers(1, 257)), int(rng.integers(1, 40)), int(rng.integers(1, 300)),
+                                      int(rng.integers(1, 70))))
+    r = subprocess.run([checker], input="closed\n" + "\n".join(lines) + "\n", capture_output=True, text=True)
+    assert r.returncode == 0 and r.stdout.startswith("ok closed cases=%d" % len(lines)), r.stdout

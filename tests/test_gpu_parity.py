@@ -409,6 +409,7 @@ def test_group_matches_oracle_and_single_launches(ctx):
             host.append((t, x16))
     torch.cuda.synchronize()
     g = mnb_hip.Group(ctx, entries)
+    assert g.plan().kernel == mnb_hip.MNB_KERNEL_STREAM and g.plan().order == mnb_hip.MNB_ORDER_NONE
     for rep in range(3):     # replays overwrite the same outputs
         g.run(st.cuda_stream)
         torch.cuda.synchronize()
@@ -429,10 +430,16 @@ def test_group_matches_oracle_and_single_launches(ctx):
         w.close()
 
 
-def _check_prefill_group(ctx, specs, seed, bs=32):
+GEMM, GEMV_GROUP = mnb_hip.MNB_KERNEL_GEMM, mnb_hip.MNB_KERNEL_GEMV_GROUP
+STREAM_K, TILE_LIST, NO_ORDER = mnb_hip.MNB_ORDER_STREAM_K, mnb_hip.MNB_ORDER_TILE_LIST, mnb_hip.MNB_ORDER_NONE
+
+
+def _check_prefill_group(ctx, specs, seed, bs=32, plan=None):
     """Records the products `specs` (M, K, N, y dtype, y +=) as groups (one
     per accumulate flag) and checks every item against the oracle on sampled
-    rows and against its own single launch, with replays bitwise identical."""
+    rows and against its own single launch, with replays bitwise identical.
+    `plan` (kernel, order, tile rows, tile columns) is the schedule every
+    group must have recorded (mnb_group_plan)."""
     import torch
     entries, host = [], []
     st = torch.cuda.Stream()
@@ -449,6 +456,8 @@ def _check_prefill_group(ctx, specs, seed, bs=32):
         if not items:
             continue
         g = mnb_hip.Group(ctx, items, accumulate=acc_group)
+        if plan is not None:
+            assert g.plan().as_tuple() == plan, (g.plan().as_tuple(), plan)
         outs = []
         for rep in range(3):
             with torch.cuda.stream(st):
@@ -485,7 +494,7 @@ def test_group_of_prefill_products(ctx):
     specs = [(200, 3072, 1000, np.float16, False), (64, 8192, 3072, np.float32, False),
              (512, 3072, 9216, np.float16, False), (33, 1536, 577, np.float32, True),
              (300, 576, 1536, np.float16, False)]
-    entries = _check_prefill_group(ctx, specs, 1200)
+    entries = _check_prefill_group(ctx, specs, 1200, plan=(GEMM, STREAM_K, 128, 256))
     with pytest.raises(mnb_hip.MnbError):       # M <= 16 and M > 16 do not mix
         mnb_hip.Group(ctx, [entries[0], (entries[1][0], torch.zeros((2, 8192), dtype=torch.float16, device="cuda"),
                                          torch.zeros((2, 3072), dtype=torch.float32, device="cuda"))])
@@ -508,7 +517,7 @@ def test_group_of_prefill_products_in_tile_list_order(ctx):
     # at 512 columns the group has 589 tiles, fewer than four per workgroup:
     # it runs with 256-column tiles
     assert sum(((M + 127) // 128) * ((N + 511) // 512) for M, K, N, _, _ in specs) < 1024
-    for w, _, _ in _check_prefill_group(ctx, specs, 1500):
+    for w, _, _ in _check_prefill_group(ctx, specs, 1500, plan=(GEMM, TILE_LIST, 128, 256)):
         w.close()
 
 
@@ -520,7 +529,7 @@ def test_group_of_prefill_products_with_wide_tiles(ctx):
     specs = [(2048, 1536, 16384, np.float16, False), (4500, 256, 8000, np.float32, False),
              (700, 576, 8000, np.float16, False), (64, 200, 30000, np.float16, False)]
     assert sum(((M + 127) // 128) * ((N + 511) // 512) for M, K, N, _, _ in specs) == 1243
-    for w, _, _ in _check_prefill_group(ctx, specs, 1700):
+    for w, _, _ in _check_prefill_group(ctx, specs, 1700, plan=(GEMM, TILE_LIST, 128, 512)):
         w.close()
 
 
@@ -530,7 +539,7 @@ def test_group_with_wide_tiles_other_block_sizes(ctx, bs):
     128, with zero points): 2096 tiles, whole and ragged."""
     specs = [(4500, 256, 16000, np.float16, False), (2048, 256, 30000, np.float16, False)]
     assert sum(((M + 127) // 128) * ((N + 511) // 512) for M, K, N, _, _ in specs) == 2096
-    for w, _, _ in _check_prefill_group(ctx, specs, 2100 + bs, bs):
+    for w, _, _ in _check_prefill_group(ctx, specs, 2100 + bs, bs, plan=(GEMM, TILE_LIST, 128, 512)):
         w.close()
 
 
@@ -562,7 +571,7 @@ def test_small_groups_of_multi_row_products(ctx, ms):
     specs = [(M, K, N, ydt, False) for M, (K, N, ydt) in zip(ms, shapes)]
     specs.append((ms[-1], 2048, 300, np.float32, True))
     assert sum((N + 511) // 512 for M, K, N, _, _ in specs) < 1024
-    for w, _, _ in _check_prefill_group(ctx, specs, 2500 + sum(ms)):
+    for w, _, _ in _check_prefill_group(ctx, specs, 2500 + sum(ms), plan=(GEMV_GROUP, NO_ORDER, 0, 16)):
         w.close()
 
 
@@ -575,7 +584,7 @@ def test_group_of_products_with_64_row_tiles(ctx):
     specs = [(64, 256, 200000, np.float16, False), (33, 200, 150001, np.float32, False),
              (48, 1000, 120000, np.float16, False), (40, 64, 100000, np.float16, False)]
     assert sum((N + 511) // 512 for M, K, N, _, _ in specs) == 1115
-    for w, _, _ in _check_prefill_group(ctx, specs, 2700):
+    for w, _, _ in _check_prefill_group(ctx, specs, 2700, plan=(GEMM, TILE_LIST, 64, 512)):
         w.close()
 
 
@@ -588,7 +597,7 @@ def test_group_of_skinny_products_as_weight_stream(ctx):
     specs = [(16, 256, 200000, np.float16, False), (7, 200, 150001, np.float32, False),
              (2, 64, 100000, np.float16, False), (9, 1000, 120000, np.float16, False)]
     assert sum((N + 511) // 512 for M, K, N, _, _ in specs) == 1115
-    for w, _, _ in _check_prefill_group(ctx, specs, 2300):
+    for w, _, _ in _check_prefill_group(ctx, specs, 2300, plan=(GEMM, TILE_LIST, 32, 512)):
         w.close()
 
 
@@ -598,7 +607,7 @@ def test_group_of_short_products_with_32_row_tiles(ctx):
     specs = [(32, 512, 150000, np.float16, False), (17, 256, 200000, np.float32, False),
              (24, 128, 250000, np.float16, False)]
     assert sum((N + 511) // 512 for M, K, N, _, _ in specs) == 1173
-    for w, _, _ in _check_prefill_group(ctx, specs, 2400):
+    for w, _, _ in _check_prefill_group(ctx, specs, 2400, plan=(GEMM, TILE_LIST, 32, 512)):
         w.close()
 
 
@@ -607,7 +616,7 @@ def test_single_item_group_in_tile_list_order(ctx):
     comes from the launch parameters rather than the table while the
     workgroups walk a tile list."""
     specs = [(512, 256, 200000, np.float16, False)]
-    for w, _, _ in _check_prefill_group(ctx, specs, 2500):
+    for w, _, _ in _check_prefill_group(ctx, specs, 2500, plan=(GEMM, TILE_LIST, 128, 512)):
         w.close()
 
 
@@ -619,7 +628,7 @@ def test_group_of_prefill_products_accumulating_in_tile_list_order(ctx):
     specs = [(2000, 384, 16001, np.float32, True), (1500, 256, 30000, np.float16, True),
              (900, 640, 12000, np.float16, True)]
     assert sum(((M + 127) // 128) * ((N + 511) // 512) for M, K, N, _, _ in specs) == 1412
-    for w, _, _ in _check_prefill_group(ctx, specs, 1900):
+    for w, _, _ in _check_prefill_group(ctx, specs, 1900, plan=(GEMM, TILE_LIST, 128, 512)):
         w.close()
 
 
@@ -713,5 +722,78 @@ def test_single_products_with_a_k_tail_not_a_multiple_of_8(ctx, K):
                     w.matmul(xd, yd)
                     torch.cuda.synchronize()
                     assert_parity(yd.cpu().numpy(), y_ref, x16, t, wmax, False, label + " device %s" % xdt)
+        finally:
+            w.close()
+
+
+@pytest.mark.parametrize("case", [(500, 3000, 32001, 32, True, False, np.float32, False),
+                                  (2048, 1024, 16384, 64, False, False, np.float16, True),
+                                  (512, 3072, 32064, 128, False, True, np.float16, False)],
+                         ids=["M500-K3000-N32001", "M2048-K1024-N16384-acc", "M512-K3072-N32064-f32scales"])
+def test_single_products_in_closed_form_tile_order(ctx, case):
+    """Single products with many 128 x 512 tiles run in tile-list order with
+    the list computed in the kernel from the tile count (no table, so the call
+    still allocates nothing): M, N and K tails, zero points, fp32 scales not
+    fp16-exact (so kept fp32), fp16 and fp32 outputs, y +=.  Sampled outputs
+    against the oracle, repeat calls bitwise identical."""
+    import torch
+    M, K, N, bs, zp, f32s, ydt, acc = case
+    t = synth.make_weight(8600 + M + N, N, K, bs, with_zp=zp)
+    w = upload(ctx, t, as_f32_scales=f32s)
+    if f32s:    # scales that fp16 cannot hold: the device keeps fp32 scales
+        s = t.scales_f16.astype(np.float32) * np.float32(1.0 + 2.0 ** -14)
+        w.close()
+        w = mnb_hip.Weight(ctx, N, K, bs, t.q, s)
+    try:
+        p = w.plan(M)
+        assert p.as_tuple() == (GEMM, TILE_LIST, 128, 512), p.as_tuple()
+        x16 = synth.make_x(8700 + M, M, K)
+        y0 = np.random.default_rng(8800 + M).standard_normal((M, N)).astype(ydt)
+        xd = torch.from_numpy(x16).cuda()
+        outs = []
+        for _ in range(2):
+            yd = torch.from_numpy(y0.copy()).cuda()
+            torch.cuda.synchronize()
+            w.matmul(xd, yd, accumulate=acc)
+            torch.cuda.synchronize()
+            outs.append(yd.cpu().numpy())
+        assert np.array_equal(outs[0].view(np.uint8), outs[1].view(np.uint8))
+        rng = np.random.default_rng(8900 + M)
+        rows = np.sort(np.concatenate([rng.choice(M, 40, replace=False), [M - 1]]))
+        cols = np.sort(np.concatenate([rng.choice(N - 16, 48, replace=False), np.arange(N - 16, N)]))
+        if f32s:
+            kb = t.kb
+            z = synth.zp_row_padded_to_flat(np.full((N, (kb + 1) // 2), 0x88, np.uint8), N, kb)
+            q2 = t.q.reshape(N, -1)[cols].reshape(-1)
+            sc = s.reshape(N, kb)[cols].reshape(-1)
+            z2 = synth.zp_row_padded_to_flat(np.full((cols.size, (kb + 1) // 2), 0x88, np.uint8), cols.size, kb)
+            xp = np.zeros((rows.size, kb * bs), np.float32)
+            xp[:, :K] = x16[rows].astype(np.float32)
+            y_ref = orc.matmul(q2, sc, z2, cols.size, kb * bs, bs, xp, threads=THREADS)
+            wmax = float(np.abs(sc).max()) * 8.0
+        else:
+            y_ref, wmax = oracle_matmul(t, np.ascontiguousarray(x16[rows]), cols, want_wmax=False)
+            wmax = None
+        got = outs[0].astype(np.float32)[np.ix_(rows, cols)] - (y0.astype(np.float32)[np.ix_(rows, cols)] if acc else 0)
+        assert_parity(got, y_ref, x16, t, wmax, ydt == np.float16 or acc,
+                      "closed-form single M=%d K=%d N=%d bs=%d" % (M, K, N, bs))
+    finally:
+        w.close()
+
+
+def test_matmul_plan_reports_the_single_product_schedule(ctx):
+    """mnb_matmul_plan: the GEMV kernel up to M = 16, stream-K 128 x 256 tiles
+    for products with few tiles, closed-form 128 x 512 tile lists for
+    products with many (the Phi-3 lm_head at M = 512 and gate_up at 2048)."""
+    for (K, N, M), expect in [((3072, 9216, 1), (mnb_hip.MNB_KERNEL_GEMV, NO_ORDER, 0, 16)),
+                              ((3072, 9216, 16), (mnb_hip.MNB_KERNEL_GEMV, NO_ORDER, 0, 16)),
+                              ((3072, 3072, 512), (GEMM, STREAM_K, 128, 256)),
+                              ((8192, 3072, 128), (GEMM, STREAM_K, 128, 256)),
+                              ((3072, 32064, 512), (GEMM, TILE_LIST, 128, 512)),
+                              ((3072, 16384, 2048), (GEMM, TILE_LIST, 128, 512))]:
+        t = synth.make_weight(1, N, K, 32)
+        w = upload(ctx, t)
+        try:
+            assert w.plan(M).as_tuple() == expect, (K, N, M, w.plan(M).as_tuple())
         finally:
             w.close()

@@ -580,6 +580,31 @@ int64_t mnb_weight_device_bytes(const mnb_weight *w) { return w ? w->bytes : 0; 
 
 int32_t mnb_supports_batch(const mnb_weight *w) { return w ? 1 : 0; }
 
+int32_t mnb_matmul_plan(const mnb_context *ctx, const mnb_weight *w, int32_t M, mnb_plan_info *out) {
+    if (!ctx || !w) return fail(MNB_ERR_INVALID_STATE, "Kernel not prepared");
+    if (!out) return fail(MNB_ERR_INVALID_ARGUMENT, "out must not be null");
+    if (M < 1 || M > mnb_max_batch_rows()) return fail(MNB_ERR_INVALID_ARGUMENT, "M out of range [1, %d]: %d", mnb_max_batch_rows(), M);
+    *out = mnb_plan_info{};
+    const WeightGeom &g = w->g;
+    if (M <= mnb::kSkinnyMaxM) {
+        out->kernel = MNB_KERNEL_GEMV;
+        out->tile_cols = mnb::kTileRows;
+        out->workgroups = g.NT;
+        return ok();
+    }
+    // the first chunk of x rows (see launch_prefill)
+    const int32_t ldx = (g.K + 7) & ~7;
+    const int64_t chunk_rows = std::max<int64_t>(128, (((int64_t)1 << 31) / ((int64_t)ldx * 2)) / 128 * 128);
+    const int32_t Mc = (int32_t)std::min<int64_t>(M, chunk_rows);
+    const mnb::SinglePlan p = mnb::sk_single_plan(Mc, g.NT, g.ST, g.scale_f32, g.SPS, ctx->cu_count);
+    out->kernel = MNB_KERNEL_GEMM;
+    out->order = p.closed ? MNB_ORDER_TILE_LIST : MNB_ORDER_STREAM_K;
+    out->tile_rows = 32 * p.fm;
+    out->tile_cols = 128 * p.ntw;
+    out->workgroups = p.closed ? std::min(p.G, mnb::sk_tiles(Mc, g.NT, p.ntw, p.fm)) : p.G;
+    return ok();
+}
+
 int32_t mnb_max_batch_rows(void) { return std::numeric_limits<int32_t>::max() / 2; }
 
 }  // extern "C"
@@ -602,8 +627,9 @@ static hipError_t launch_prefill(const mnb_weight *w, int cu_count, const mnb::M
         c.M = std::min(chunk, a.M - m0);
         c.x = a.x + (size_t)m0 * a.ldx;
         c.y = (unsigned char *)a.y + (size_t)m0 * y_row;
-        const int G = mnb::sk_grid(mnb::sk_tiles(c.M, g.NT), g.ST, cu_count);
-        const hipError_t e = mnb::launch_gemm_sk(w, c, G, ws, s);
+        const mnb::SinglePlan plan = mnb::sk_single_plan(c.M, g.NT, g.ST, g.scale_f32, g.SPS, cu_count);
+        const hipError_t e = plan.closed ? mnb::launch_gemm_closed(w, c, plan.ntw, plan.fm, plan.G, s)
+                                         : mnb::launch_gemm_sk(w, c, plan.G, ws, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -748,9 +774,6 @@ struct mnb_group {
 constexpr int kGemmListTilesPerWg = 4;
 // Largest M of a group's items for 32-row tiles, and for 64-row tiles.
 constexpr int kGemmSkinnyMaxM = 32, kGemmHalfMaxM = 64;
-// Cost of a 512-column stage in 256-column stages (same-box A/B of the M=512
-// group: 1046 vs 1155 TFLOP/s, so 2 / 1.105).
-constexpr double kGemmWideStageCost = 1.81;
 // Cost of a 64 x 512 stage in 128 x 256 stages: the same MFMA work and the
 // same operand bytes (x and weights trade places), rounded up.
 constexpr double kGemmHalfStageCost = 1.1;
@@ -855,7 +878,7 @@ static int32_t group_create_gemm(mnb_context *ctx, int32_t count, const mnb_grou
             std::vector<mnb::SkRange> wg_w;
             if (build(mnb::kGemmWideNTW) && tiles >= min_tiles) {
                 mnb::sk_tile_list(plan.host, plan.G, seq_w, wg_w);
-                if ((double)busiest(wg_w) * kGemmWideStageCost < narrow) {
+                if ((double)busiest(wg_w) * mnb::kGemmWideStageCost < narrow) {
                     seq.swap(seq_w);
                     wg.swap(wg_w);
                 } else {
@@ -1026,6 +1049,28 @@ int32_t mnb_group_run(mnb_context *ctx, const mnb_group *group, void *stream) {
     }
     hipError_t e = group->plan.m1 ? mnb::launch_gemv_stream(group->plan, s) : mnb::launch_gemv_group(group->plan, s);
     if (e != hipSuccess) return hip_fail(e, "matvec");
+    return ok();
+}
+
+int32_t mnb_group_plan(const mnb_group *group, mnb_plan_info *out) {
+    if (!group || !out) return fail(MNB_ERR_INVALID_ARGUMENT, "group and out must not be null");
+    *out = mnb_plan_info{};
+    if (group->gemm) {
+        const mnb::GemmGroupPlan &g = group->gplan;
+        out->kernel = MNB_KERNEL_GEMM;
+        out->order = g.seq ? MNB_ORDER_TILE_LIST : MNB_ORDER_STREAM_K;
+        out->tile_rows = 32 * g.fm;
+        out->tile_cols = 128 * g.ntw;
+        out->workgroups = g.G;
+    } else if (group->plan.m1) {
+        out->kernel = MNB_KERNEL_STREAM;
+        out->tile_cols = mnb::kTileRows;
+        out->workgroups = group->plan.stream_wgs;
+    } else {
+        out->kernel = MNB_KERNEL_GEMV_GROUP;
+        out->tile_cols = mnb::kTileRows;
+        out->workgroups = group->plan.total_wgs;
+    }
     return ok();
 }
 

@@ -96,6 +96,7 @@ struct SkParams {
     const SkTile *seq;      // tile-list order: the tiles, workgroup-major (else nullptr)
     const SkRange *wg;      // tile-list order: G + 1 workgroup starts
     int32_t count;
+    int32_t closed;         // 1: tile-list order of the single item `one` in closed form (sk_cf_*), no table
     int32_t G;              // workgroups
     int32_t I;              // iterations of all items (below 2^31)
     float *ws;              // [G][2] partial tiles: slot 0 for a workgroup's first tile, 1 for its last
@@ -148,14 +149,21 @@ __device__ __forceinline__ SkRange sk_wg(const SkParams &p, int g) {
 // first iteration of logical workgroup g (g = G gives I)
 __device__ __forceinline__ int sk_start(int g, const SkParams &p) {
     if (p.seq) return sk_wg(p, g).iter;
+    if (p.closed) return sk_cf_first(p.one.T, p.G, g) * p.one.ST;
     return (int)((int64_t)g * p.I / p.G);
 }
 
 // A cursor over the launch's tiles is item ci (fields ic), tile t of that
-// item and, in tile-list order, the list position pos.  Steps it to the next
-// tile of the launch (the caller knows there is one).
-__device__ __forceinline__ void sk_next_tile(const SkParams &p, int &ci, int &t, int &pos, SkItem &ic) {
-    if (p.seq) {
+// item and, in tile-list order, the list position pos (closed form: the
+// workgroup's own tile count so far, its tiles at block-order positions
+// cf_base + pos * cf_step).  Steps it to the next tile of the launch (the
+// caller knows there is one).
+__device__ __forceinline__ void sk_next_tile(const SkParams &p, int &ci, int &t, int &pos, SkItem &ic, int cf_base,
+                                             int cf_step) {
+    if (p.closed) {
+        ++pos;
+        t = sk_cf_tile(ic.MT, ic.T / ic.MT, cf_base + pos * cf_step);
+    } else if (p.seq) {
         const SkTile e = sk_seq(p, ++pos);
         if (e.item != ci) {
             ci = e.item;
@@ -170,6 +178,7 @@ __device__ __forceinline__ void sk_next_tile(const SkParams &p, int &ci, int &t,
 
 // k extent of the tile after the cursor's (the caller knows there is one).
 __device__ __forceinline__ int sk_next_kx(const SkParams &p, int ci, int t, int pos, const SkItem &ic) {
+    if (p.closed) return ic.kx;
     if (p.seq) {
         const int item = sk_seq(p, pos + 1).item;
         return item == ci ? ic.kx : sk_item(p, item).kx;
@@ -301,7 +310,13 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     // compute cursor: the tile (item fields ic, tile t of the item) and the
     // stage cst of the tile
     int ci, t, cpos, cst;
-    if (p.seq) {
+    const int cf_base = p.closed ? sk_cf_base(p.one.T, p.G, g) : 0, cf_step = sk_cf_step(p.G);
+    if (p.closed) {
+        cpos = 0;
+        ci = 0;
+        t = sk_cf_tile(p.one.MT, p.one.T / p.one.MT, cf_base);
+        cst = 0;
+    } else if (p.seq) {
         cpos = sk_wg(p, g).pos;
         const SkTile e = sk_seq(p, cpos);
         ci = e.item;
@@ -312,7 +327,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
         ci = sk_find_item(p, i0);
     }
     SkItem ic = sk_item(p, ci);
-    if (!p.seq) {
+    if (!p.seq && !p.closed) {
         t = (i0 - ic.ibeg) / ic.ST;
         cst = (i0 - ic.ibeg) - t * ic.ST;
     }
@@ -383,7 +398,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             ++li;
             if (++lst == iq.ST) {
                 lst = 0;
-                sk_next_tile(p, ii, lt, ipos, iq);
+                sk_next_tile(p, ii, lt, ipos, iq, cf_base, cf_step);
                 set_tile();
             }
         }
@@ -531,19 +546,23 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             }
         } else if constexpr (NTW == kSkNTW && FM == kSkFM) {
             // partial tile of a split tile: [BM][kSkBN] fp32, summed by sk_reduce_kernel
-            // (wide, half and skinny tiles run in tile-list order only, where no tile is split)
+            // (wide, half and skinny tiles run in tile-list order only, where no tile is split);
+            // rows past M are neither stored nor summed
             const int slot = first_seg ? 0 : 1;
             __attribute__((address_space(1))) float *part =
                 (__attribute__((address_space(1))) float *)p.ws + ((size_t)g * 2 + slot) * kSkPartialFloats;
 #pragma unroll
             for (int a = 0; a < FM; ++a)
+                if (m0 + a * 32 + c32 < ic.M) {
 #pragma unroll
-                for (int f = 0; f < FN; ++f)
+                    for (int f = 0; f < FN; ++f)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        *(__attribute__((address_space(1))) float4_t *)(part + (a * 32 + c32) * kSkBN + c_wave + f * 32 +
-                                                                         8 * j + 4 * h) =
-                            (float4_t){acc[a][f][4 * j], acc[a][f][4 * j + 1], acc[a][f][4 * j + 2], acc[a][f][4 * j + 3]};
+                        for (int j = 0; j < 4; ++j)
+                            *(__attribute__((address_space(1))) float4_t *)(part + (a * 32 + c32) * kSkBN + c_wave +
+                                                                             f * 32 + 8 * j + 4 * h) =
+                                (float4_t){acc[a][f][4 * j], acc[a][f][4 * j + 1], acc[a][f][4 * j + 2],
+                                           acc[a][f][4 * j + 3]};
+                }
         }
 #pragma unroll
         for (int a = 0; a < FM; ++a)
@@ -710,7 +729,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             remaining -= seg_n;
             epilogue(seg_n);
             if (remaining == 0) break;
-            sk_next_tile(p, ci, t, cpos, ic);
+            sk_next_tile(p, ci, t, cpos, ic, cf_base, cf_step);
             seg_n = min(remaining, ic.ST);
             kk = 0;
         }
@@ -751,7 +770,10 @@ __global__ __launch_bounds__(kSkReduceThreads) void sk_reduce_kernel(SkParams p)
     const int c = (tid % kColGroups) * 4;
     const int r0 = rb * kSkReduceRows + tid / kColGroups;
     const int m0 = (t % it.MT) * kSkBM, n = (t / it.MT) * kSkBN + c;
-    if (n >= it.N) return;
+    // rows past M hold no partial sums (the GEMM does not store them): a
+    // workgroup whose 16 rows all lie past M has nothing to do; in the block
+    // that M cuts, the loads of rows past M read values that are never stored
+    if (n >= it.N || m0 + rb * kSkReduceRows >= it.M) return;
     float4_t sum[kRowsPerThread];
     auto part = [&](int i, int k) __attribute__((always_inline)) {
         return gld((const float4_t *)(p.ws + (size_t)s_part[i] * kSkPartialFloats +
@@ -836,6 +858,21 @@ int sk_grid(int T, int ST, int cu_count) {
     return (int)best;
 }
 
+SinglePlan sk_single_plan(int M, int NT, int ST, int scale_f32, int sps, int cu_count) {
+    const int T = sk_tiles(M, NT);
+    SinglePlan plan{false, kSkNTW, kSkFM, sk_grid(T, ST, cu_count)};
+    if (!sk_wide_supported(scale_f32, sps)) return plan;
+    const double stream_k = sk_cost(T, ST, plan.G, cu_count);
+    const int Tw = sk_tiles(M, NT, kSkWideNTW, kSkFM);
+    const int Gw = std::min(std::min(cu_count, kSkReduceThreads), Tw);
+    int busiest = 0;   // tiles of the busiest workgroup in closed-form order
+    for (int g = 0; g < Gw; ++g) busiest = std::max(busiest, sk_cf_first(Tw, Gw, g + 1) - sk_cf_first(Tw, Gw, g));
+    const double load = (double)Gw / cu_count;
+    const double wide = busiest * (ST * (1.16 + 0.38 * load) * kGemmWideStageCost + 8.6);
+    if (wide < stream_k) plan = SinglePlan{true, kSkWideNTW, kSkFM, Gw};
+    return plan;
+}
+
 SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg, int ntw, int fm) {
     const WeightGeom &g = w->g;
     SkItem it{};
@@ -881,20 +918,22 @@ static void launch_sk_variant(int ntw, int fm, dim3 grid, dim3 block, hipStream_
 // `items` with host copy `host`) and, when some workgroup range boundary falls
 // inside a tile, the reduce kernel.
 static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem *host, int32_t count,
-                            const SkTile *seq, const SkRange *wg, int ntw, int fm, int64_t iters, int scale_f32,
-                            int has_zp, int sps, int G, float *ws, hipStream_t stream) {
+                            const SkTile *seq, const SkRange *wg, bool closed, int ntw, int fm, int64_t iters,
+                            int scale_f32, int has_zp, int sps, int G, float *ws, hipStream_t stream) {
     if (iters >= (int64_t)1 << 31 || G < 1 || G > kSkReduceThreads) return hipErrorInvalidValue;
+    if (closed && (count != 1 || seq)) return hipErrorInvalidValue;
     // 256 x 128 tiles, or wide (512 x 128), half (512 x 64) and skinny (512 x 32) tiles in
     // tile-list order only (no split tiles, no partial tiles)
     const bool narrow = ntw == kSkNTW && fm == kSkFM;
     const bool wide = ntw == kSkWideNTW && (fm == kSkFM || fm == kSkHalfFM || fm == kSkSkinnyFM);
-    if (!narrow && (!wide || !seq || !sk_wide_supported(scale_f32, sps))) return hipErrorInvalidValue;
+    if (!narrow && (!wide || !(seq || closed) || !sk_wide_supported(scale_f32, sps))) return hipErrorInvalidValue;
     SkParams p;
     p.one = one;
     p.items = items;
     p.seq = seq;
     p.wg = wg;
     p.count = count;
+    p.closed = closed ? 1 : 0;
     p.G = G;
     p.I = (int32_t)iters;
     p.ws = ws;
@@ -921,7 +960,7 @@ static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem
     // in tile-list order)
     bool split = false;
     int32_t k = 0;
-    for (int b = 1; b < G && !split && !seq; ++b) {
+    for (int b = 1; b < G && !split && !seq && !closed; ++b) {
         const int64_t s = (int64_t)b * iters / G;
         while (k + 1 < count && host[k + 1].ibeg <= s) ++k;
         split = (s - host[k].ibeg) % host[k].ST != 0;
@@ -936,13 +975,20 @@ static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem
 hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, hipStream_t stream) {
     const WeightGeom &g = w->g;
     const SkItem one = sk_make_item(w, a, 0);
-    return launch_sk(one, nullptr, &one, 1, nullptr, nullptr, kSkNTW, kSkFM, (int64_t)one.T * g.ST, g.scale_f32,
+    return launch_sk(one, nullptr, &one, 1, nullptr, nullptr, false, kSkNTW, kSkFM, (int64_t)one.T * g.ST, g.scale_f32,
                      g.has_zp, g.SPS, G, ws, stream);
+}
+
+hipError_t launch_gemm_closed(const mnb_weight *w, const MatmulArgs &a, int ntw, int fm, int G, hipStream_t stream) {
+    const WeightGeom &g = w->g;
+    const SkItem one = sk_make_item(w, a, 0, ntw, fm);
+    return launch_sk(one, nullptr, &one, 1, nullptr, nullptr, true, ntw, fm, (int64_t)one.T * g.ST, g.scale_f32,
+                     g.has_zp, g.SPS, std::min(G, one.T), nullptr, stream);
 }
 
 hipError_t launch_gemm_group(const GemmGroupPlan &g, float *ws, hipStream_t stream) {
     return launch_sk(g.host[0], (const SkItem *)g.items, g.host.data(), g.count, (const SkTile *)g.seq,
-                     (const SkRange *)g.wg, g.ntw, g.fm, g.iters, g.scale_f32, g.has_zp, g.sps, g.G, ws, stream);
+                     (const SkRange *)g.wg, false, g.ntw, g.fm, g.iters, g.scale_f32, g.has_zp, g.sps, g.G, ws, stream);
 }
 
 }  // namespace mnb

@@ -215,6 +215,9 @@ constexpr int kStreamWavesPerBlock = 4;
 // order only)
 constexpr int kGemmNTW = 2, kGemmWideNTW = 4;
 constexpr int kGemmFM = 4, kGemmHalfFM = 2, kGemmSkinnyFM = 1;
+// Cost of a 512-column stage in 256-column stages (same-box A/B of the M=512
+// group: 1046 vs 1155 TFLOP/s, so 2 / 1.105).
+constexpr double kGemmWideStageCost = 1.81;
 
 // A recorded group of independent products with M > 16 (all items share the
 // kernel variant): one launch over all their iterations, in stream-K order
@@ -243,6 +246,21 @@ bool sk_wide_supported(int scale_f32, int sps);
 // whole tiles per workgroup when that is cheapest, else stream-K).
 int sk_grid(int T, int ST, int cu_count);
 hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, hipStream_t stream);
+// One product in tile-list order with whole tiles of 32 fm rows x 128 ntw
+// columns on min(G, tiles) workgroups, the list in closed form (sk_cf_*): no
+// table, no split tile, no workspace.  Wide tiles (ntw = kGemmWideNTW) need
+// sk_wide_supported.
+hipError_t launch_gemm_closed(const mnb_weight *w, const MatmulArgs &a, int ntw, int fm, int G, hipStream_t stream);
+// How one product with M > 16 runs: stream-K over 128 x 256 tiles on sk_grid
+// workgroups, or whole 128 x 512 tiles in closed-form tile-list order when
+// the cost model of sk_grid, with a 512-column stage costing
+// kGemmWideStageCost 256-column stages, expects the busiest workgroup to
+// finish first that way.
+struct SinglePlan {
+    bool closed;
+    int ntw, fm, G;
+};
+SinglePlan sk_single_plan(int M, int NT, int ST, int scale_f32, int sps, int cu_count);
 SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg, int ntw = kGemmNTW, int fm = kGemmFM);
 hipError_t launch_gemm_group(const GemmGroupPlan &g, float *ws, hipStream_t stream);
 

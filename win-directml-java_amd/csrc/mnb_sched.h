@@ -6,6 +6,12 @@
 
 #include <vector>
 
+#if defined(__HIPCC__)
+#define MNB_HD __host__ __device__
+#else
+#define MNB_HD
+#endif
+
 namespace mnb {
 
 // One product of a GEMM launch (M > 16): the weight's tiled buffers, x, y and
@@ -45,6 +51,58 @@ struct SkRange {
 // entries; workgroup g owns seq[wg[g].pos, wg[g + 1].pos), whose stages are
 // the iterations [wg[g].iter, wg[g + 1].iter)).
 void sk_tile_list(const std::vector<SkItem> &items, int G, std::vector<SkTile> &seq, std::vector<SkRange> &wg);
+
+// The tile list of ONE item in closed form: exactly what sk_tile_list gives a
+// launch of a single item (every tile costs the same, so each XCD's chunk is
+// dealt round robin), computed from the tile count instead of read from a
+// table, so a single product can run in tile-list order without a device
+// table.  X = 8 XCDs when G is a multiple of 8, else 1; per = G / X logical
+// workgroups per XCD; the item's tiles in block order are cut at
+// sk_cf_xcd_start(T, X, x), and logical workgroup g = x * per + r owns the
+// block-order positions sk_cf_xcd_start(T, X, x) + r + j * per below the next
+// XCD's start.
+MNB_HD inline int32_t sk_cf_xcd_start(int32_t T, int32_t X, int32_t x) {
+    // tile i goes to XCD min(X - 1, floor((2 i + 1) X / (2 T))) (the equal-cost
+    // cut of sk_tile_list), so XCD x starts at ceil((2 T x - X) / (2 X))
+    if (x <= 0) return 0;
+    if (x >= X) return T;
+    const int64_t v = 2 * (int64_t)T * x - X;
+    return v <= 0 ? 0 : (int32_t)((v + 2 * X - 1) / (2 * X));
+}
+// Tiles owned by the logical workgroups before g (g = G gives T).
+MNB_HD inline int32_t sk_cf_first(int32_t T, int32_t G, int32_t g) {
+    const int32_t X = G % 8 == 0 ? 8 : 1, per = G / X, x = g / per, r = g % per;
+    const int32_t c = sk_cf_xcd_start(T, X, x), L = sk_cf_xcd_start(T, X, x + 1) - c;
+    return c + (L / per) * r + (r < L % per ? r : L % per);
+}
+// Block-order position of logical workgroup g's first tile; its j-th tile
+// is at that position + j * per.
+MNB_HD inline int32_t sk_cf_base(int32_t T, int32_t G, int32_t g) {
+    const int32_t X = G % 8 == 0 ? 8 : 1, per = G / X;
+    return sk_cf_xcd_start(T, X, g / per) + g % per;
+}
+MNB_HD inline int32_t sk_cf_step(int32_t G) { return G % 8 == 0 ? G / 8 : G; }
+// Tile (m-tile + n-group * MT) at block-order position q of an item with MT
+// m-tiles and NG n-groups: chunks of up to 4 m-tiles, each cut into blocks of
+// 32 / (its m-tiles) n-groups, a block's tiles m-tile-major.
+MNB_HD inline int32_t sk_cf_tile(int32_t MT, int32_t NG, int32_t q) {
+    const int32_t full = MT / 4;
+    int32_t m0, mc, local;
+    if (q < full * 4 * NG) {
+        const int32_t c = q / (4 * NG);
+        m0 = 4 * c;
+        mc = 4;
+        local = q - c * 4 * NG;
+    } else {
+        m0 = full * 4;
+        mc = MT - m0;
+        local = q - full * 4 * NG;
+    }
+    const int32_t nb = 32 / mc, blk = local / (mc * nb), n0 = blk * nb;
+    const int32_t nn = NG - n0 < nb ? NG - n0 : nb;
+    const int32_t within = local - blk * mc * nb;
+    return m0 + within / nn + (n0 + within % nn) * MT;
+}
 
 // Static schedule of a group of M = 1 products on the persistent streaming
 // kernel (mnb_stream.hip).  A unit is one 16-row n-tile of one item over its

@@ -53,7 +53,7 @@ EXPORTED_SYMBOLS = (
     "mnb_version", "mnb_last_error", "mnb_context_create", "mnb_context_destroy", "mnb_context_info",
     "mnb_weight_create", "mnb_weight_fuse_rows", "mnb_weight_quantize", "mnb_weight_read", "mnb_weight_destroy", "mnb_weight_shape", "mnb_weight_device_bytes", "mnb_matmul", "mnb_matmul_noalloc",
     "mnb_dequantize", "mnb_supports_batch", "mnb_max_batch_rows", "mnb_device_alloc", "mnb_device_free",
-    "mnb_memcpy", "mnb_synchronize", "mnb_group_create", "mnb_group_run", "mnb_group_destroy",
+    "mnb_memcpy", "mnb_synchronize", "mnb_group_create", "mnb_group_run", "mnb_group_destroy", "mnb_matmul_plan", "mnb_group_plan",
     "mnb_pack_open", "mnb_pack_close", "mnb_pack_kind", "mnb_pack_weight_count", "mnb_pack_weight_name",
     "mnb_pack_find_projection", "mnb_pack_weight_info", "mnb_pack_read_weight", "mnb_pack_weight_create",
 )
@@ -92,6 +92,19 @@ class TripletInfo(ctypes.Structure):
     _fields_ = [("N", ctypes.c_int32), ("K", ctypes.c_int32), ("block_size", ctypes.c_int32),
                 ("blocks_per_row", ctypes.c_int32), ("q_bytes", ctypes.c_int64), ("scale_count", ctypes.c_int64),
                 ("zp_bytes", ctypes.c_int64), ("zp_implicit", ctypes.c_int32), ("scale_dtype", ctypes.c_int32)]
+
+
+MNB_KERNEL_GEMV, MNB_KERNEL_STREAM, MNB_KERNEL_GEMV_GROUP, MNB_KERNEL_GEMM = 1, 2, 3, 4
+MNB_ORDER_NONE, MNB_ORDER_STREAM_K, MNB_ORDER_TILE_LIST = 0, 1, 2
+
+
+class PlanInfo(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_int32), ("order", ctypes.c_int32), ("tile_rows", ctypes.c_int32),
+                ("tile_cols", ctypes.c_int32), ("workgroups", ctypes.c_int32)]
+
+    def as_tuple(self):
+        """(kernel, order, tile_rows, tile_cols)"""
+        return (self.kernel, self.order, self.tile_rows, self.tile_cols)
 
 
 class GroupItem(ctypes.Structure):
@@ -150,6 +163,8 @@ def load() -> ctypes.CDLL:
         "mnb_group_create": (i32, [vp, i32, ctypes.POINTER(GroupItem), ctypes.POINTER(vp)]),
         "mnb_group_run": (i32, [vp, vp, vp]),
         "mnb_group_destroy": (i32, [vp]),
+        "mnb_matmul_plan": (i32, [vp, vp, i32, ctypes.POINTER(PlanInfo)]),
+        "mnb_group_plan": (i32, [vp, ctypes.POINTER(PlanInfo)]),
         "mnb_pack_open": (i32, [ctypes.c_char_p, ctypes.POINTER(vp)]),
         "mnb_pack_close": (i32, [vp]),
         "mnb_pack_kind": (i32, [vp, ctypes.POINTER(i32)]),
@@ -353,6 +368,12 @@ class Weight:
               "matvec" if M == 1 else "matmulBatch")
         return y
 
+    def plan(self, M: int) -> PlanInfo:
+        """How mnb_matmul runs this weight at M rows (mnb_matmul_plan)."""
+        p = PlanInfo()
+        check(load().mnb_matmul_plan(self.ctx.handle, self.handle, M, ctypes.byref(p)), "plan")
+        return p
+
     def dequantize(self, dtype=np.float32, out=None, stream=None):
         """[N, K] dequantized weight; numpy (host) or a torch CUDA tensor ``out``."""
         L = load()
@@ -391,6 +412,14 @@ class Group:
         self._h = h
         self.ctx = ctx
         self._keep = entries
+
+    def plan(self) -> PlanInfo:
+        """The kernel and work order recorded for this group (mnb_group_plan)."""
+        if self._h is None:
+            raise IllegalStateException("group is closed")
+        p = PlanInfo()
+        check(load().mnb_group_plan(self._h, ctypes.byref(p)), "plan")
+        return p
 
     def run(self, stream=None) -> None:
         if self._h is None:
