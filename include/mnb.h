@@ -322,6 +322,12 @@ int32_t mnb_synchronize(mnb_context *ctx);
  *   MNB_PACK_ONNX   ONNX model; MatMulNBits inputs [A, B, scales, zero_points?]
  *                   (Q2W:534-545); external data in model.onnx_data or
  *                   model.onnx.data beside the model (QwenModelDirValidator.java:163-174).
+ *   MNB_PACK_SAFETENSORS  a *.safetensors file: dense tensors only (no
+ *                   MatMulNBits triplets), checked as SafeTensorsReader.read
+ *                   does (directml-inference/.../model/SafeTensorsReader.java:
+ *                   84-277, its IOException texts); weight names are its tensor
+ *                   names in directory order.  A dense matrix of any pack
+ *                   becomes an int4 weight with mnb_pack_weight_quantize.
  *
  * Weight names are the Phi-3 roles, or the first output of each MatMulNBits
  * node in graph order.  A triplet is resolved as the reference loads it
@@ -339,6 +345,7 @@ int32_t mnb_synchronize(mnb_context *ctx);
 #define MNB_PACK_PHI3 1
 #define MNB_PACK_QWEN2 2
 #define MNB_PACK_ONNX 3
+#define MNB_PACK_SAFETENSORS 4
 
 typedef struct mnb_pack mnb_pack;
 typedef struct mnb_triplet_info {
@@ -393,6 +400,24 @@ int32_t mnb_pack_read_weight(const mnb_pack *pack, const char *name, uint8_t *q,
  * QuantizedWeight (MNK:940-970).  A zero-point stream whose nibbles are all 8
  * is uploaded as the implicit zero point (identical values). */
 int32_t mnb_pack_weight_create(mnb_context *ctx, const mnb_pack *pack, const char *name, mnb_weight **out);
+
+/* Element type (ONNX code: 1 FLOAT, 10 FLOAT16, 16 BFLOAT16, ...) and shape
+ * of any tensor of the pack (up to dims_cap dimensions written; *ndims gets
+ * the rank).  No reference counterpart beyond the tensor catalogs of its
+ * readers (SafeTensorsReader.SafeTensorEntry, OnnxModelReader.OnnxTensor). */
+int32_t mnb_pack_tensor_info(const mnb_pack *pack, const char *name, int32_t *dtype, int64_t *dims, int32_t dims_cap,
+                             int32_t *ndims);
+
+/* The runtime-quantized tied lm_head from a weight file: the dense matrix
+ * `name` (e.g. "model.embed_tokens.weight" of a safetensors file or an ONNX
+ * model) read as the reference reads its embedding table (Q2W:599-704:
+ * FLOAT as stored, FLOAT16 through fp16ToFp32, other types fail), its shape
+ * checked against [rows, cols] ("Unexpected dimensions for ..."; Q2W:1637),
+ * then quantized on the device exactly as mnb_weight_quantize (createTiedLmHead
+ * + quantizeDenseRowsToUInt4, Q2W:1329-1422; block_size 0 is the reference's
+ * choice).  Failures to read return MNB_ERR_IO. */
+int32_t mnb_pack_weight_quantize(mnb_context *ctx, const mnb_pack *pack, const char *name, int32_t rows, int32_t cols,
+                                 int32_t block_size, mnb_weight **out);
 
 #ifdef __cplusplus
 }

@@ -193,3 +193,58 @@ def test_qwen_tied_lm_head_quantized_on_device(ctx):
             assert err <= tol
     finally:
         w.close()
+
+
+def test_tied_lm_head_quantized_from_weight_files(ctx, tmp_path):
+    """The runtime-quantized tied lm_head read from a file
+    (mnb_pack_weight_quantize): a safetensors model.embed_tokens.weight in F32
+    and in F16 (widened with the reference's fp16ToFp32, subnormal values
+    included), and an ONNX model's FLOAT16 initializer in external data.  The
+    weight's bytes equal the oracle's quantizeDenseRowsToUInt4 of the values
+    the reference's embedding table holds; BF16 is refused as the reference
+    refuses it, and a shape other than [vocab, hidden] fails with the
+    reference's text."""
+    import weightfiles as wf
+    rows, cols = 300, 896
+    rng = np.random.default_rng(11)
+    emb = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    emb[3, :40] = rng.standard_normal(40).astype(np.float32) * 1e-6     # fp16 subnormals after rounding
+    e16 = emb.astype(np.float16)
+    e16_ref = orc.fp16_bits_to_fp32(e16.view(np.uint16))              # the reference's widening
+    st = wf.write_safetensors(tmp_path / "model.safetensors",
+                              [("model.embed_tokens.weight", "F32", (rows, cols), emb.tobytes()),
+                               ("embed16", "F16", (rows, cols), e16.tobytes()),
+                               ("emb_bf16", "BF16", (rows, cols), (emb.view(np.uint32) >> 16).astype(np.uint16).tobytes())])
+    with mnb_hip.Pack(st) as pk:
+        for name, ref in (("model.embed_tokens.weight", emb), ("embed16", e16_ref)):
+            w = pk.quantize(ctx, name, rows, cols)
+            try:
+                bs = orc.choose_tied_block_size(cols)
+                assert (w.N, w.K, w.block_size) == (rows, cols, bs)
+                q, s, z = w.read()
+                rq, rs, rz = orc.quantize_rows_u4(ref, rows, cols, bs)
+                assert np.array_equal(q, rq) and np.array_equal(s.view(np.uint32), rs.view(np.uint32)), name
+                assert np.array_equal(z, rz), name
+            finally:
+                w.close()
+        with pytest.raises(mnb_hip.IOException, match=r"Unsupported inline tensor data for emb_bf16: BFLOAT16 \(16\)"):
+            pk.quantize(ctx, "emb_bf16", rows, cols)
+        with pytest.raises(mnb_hip.IOException,
+                           match=r"Unexpected dimensions for embed16: \[300, 896\], expected \[151936, 896\]"):
+            pk.quantize(ctx, "embed16", 151936, cols)
+        with pytest.raises(mnb_hip.IOException, match="Tensor not found: lm_head"):
+            pk.quantize(ctx, "lm_head", rows, cols)
+    # an ONNX model with the embedding as an external FLOAT16 initializer
+    b = wf.OnnxBuilder()
+    b.tensor("model.embed_tokens.weight", 10, [rows, cols], e16.tobytes(), external=True)
+    d = tmp_path / "onnx"
+    d.mkdir()
+    with mnb_hip.Pack(b.write(str(d))) as pk:
+        w = pk.quantize(ctx, "model.embed_tokens.weight", rows, cols, 64)
+        try:
+            q, s, z = w.read()
+            rq, rs, rz = orc.quantize_rows_u4(e16_ref, rows, cols, 64)
+            assert np.array_equal(q, rq) and np.array_equal(s.view(np.uint32), rs.view(np.uint32))
+            assert np.array_equal(z, rz)
+        finally:
+            w.close()

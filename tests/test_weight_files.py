@@ -579,3 +579,109 @@ def test_reference_phi3_export_resolves_every_matmulnbits_triplet(tmp_path):
         assert pk.info("logits").N == 32064
         q, s, z = pk.read(pk.find_projection(0, "q_proj"))
         assert q.size == 3072 * 24 * 64 and s.size == 3072 * 24 and z.size == 3072 * 24 // 2
+
+
+# ---------------------------------------------------------------------------
+# SafeTensors files (SafeTensorsReader.java:84-277)
+# ---------------------------------------------------------------------------
+
+def test_safetensors_reference_case_parses_header_and_payload(tmp_path):
+    """SafeTensorsReaderTest.parsesHeaderAndMmapBackedPayload: an F16 [2, 2]
+    embedding with metadata; dtype code 10 (toOnnxDataType), shape, bytes."""
+    header = ('{"model.embed_tokens.weight":{"dtype":"F16","shape":[2,2],"data_offsets":[0,8]},'
+              '"__metadata__":{"format":"pt"}}')
+    p = wf.write_safetensors(tmp_path / "model.safetensors", [], header=header, tail=bytes(range(1, 9)))
+    with Pack(p) as pk:
+        assert pk.kind == mnb_hip.MNB_PACK_SAFETENSORS
+        assert pk.names() == ["model.embed_tokens.weight"]
+        assert pk.tensor_info("model.embed_tokens.weight") == (10, (2, 2))
+        with pytest.raises(IOException, match="Quantized weight not found for layer 0 q_proj"):
+            pk.find_projection(0, "q_proj")
+        with pytest.raises(IOException, match="Quantized weight not found: model.embed_tokens.weight"):
+            pk.info("model.embed_tokens.weight")
+
+
+def test_safetensors_reference_case_rejects_invalid_byte_length(tmp_path):
+    """SafeTensorsReaderTest.rejectsInvalidByteLength: F32 [2] in 4 bytes."""
+    header = '{"x":{"dtype":"F32","shape":[2],"data_offsets":[0,4]}}'
+    p = wf.write_safetensors(tmp_path / "bad.safetensors", [], header=header, tail=struct.pack("<i", 1234))
+    _err(p, "SafeTensors byte length mismatch for x in bad.safetensors: expected 8 bytes from dtype/shape, got 4")
+
+
+def test_safetensors_directory_order_dtypes_and_shapes(tmp_path):
+    """Tensors in directory order (every dtype the reader knows, with its
+    ONNX code), lower-case dtypes upper-cased, a repeated name keeping its
+    first position and last value, empty and scalar shapes."""
+    ts = [("b.f32", "F32", (3, 2), bytes(24)), ("a.bf16", "bf16", (4,), bytes(8)), ("c.u8", "U8", (), bytes(1)),
+          ("d.i64", "I64", (0, 5), b""), ("e.bool", "BOOL", (2,), bytes(2)), ("f.f64", "F64", (1,), bytes(8)),
+          ("g.i16", "I16", (1,), bytes(2)), ("h.u16", "U16", (1,), bytes(2)), ("i.u32", "U32", (1,), bytes(4)),
+          ("j.u64", "U64", (1,), bytes(8)), ("k.i8", "I8", (1,), bytes(1)), ("l.i32", "I32", (1,), bytes(4)),
+          ("m.f16", "F16", (2, 1), bytes(4))]
+    p = wf.write_safetensors(tmp_path / "m.safetensors", ts, metadata={"format": "pt"})
+    codes = {"F32": 1, "BF16": 16, "U8": 2, "I64": 7, "BOOL": 9, "F64": 11, "I16": 5, "U16": 4, "U32": 12, "U64": 13,
+             "I8": 3, "I32": 6, "F16": 10}
+    with Pack(p) as pk:
+        assert pk.names() == [t[0] for t in ts]
+        for name, dt, shape, _ in ts:
+            assert pk.tensor_info(name) == (codes[dt.upper()], tuple(shape)), name
+    dup = '{"x":{"dtype":"F32","shape":[1],"data_offsets":[0,4]},"y":{"dtype":"U8","shape":[1],"data_offsets":[4,5]},' \
+          '"x":{"dtype":"F16","shape":[2],"data_offsets":[0,4]}}'
+    with Pack(wf.write_safetensors(tmp_path / "d.safetensors", [], header=dup, tail=bytes(5))) as pk:
+        assert pk.names() == ["x", "y"] and pk.tensor_info("x") == (10, (2,))
+    with Pack(wf.write_safetensors(tmp_path / "a.safetensors", [], header="[1, 2]", tail=b"")) as pk:
+        assert pk.names() == []        # a directory that is not an object lists no tensors
+
+
+@pytest.mark.parametrize("header,tail,match", [
+    ('{"x":5}', b"", "Invalid SafeTensors tensor entry for x in e.safetensors"),
+    ('{"x":{"shape":[1],"data_offsets":[0,4]}}', bytes(4), "Invalid SafeTensors tensor x in e.safetensors: missing textual dtype"),
+    ('{"x":{"dtype":7,"shape":[1],"data_offsets":[0,4]}}', bytes(4), "missing textual dtype"),
+    ('{"x":{"dtype":"F32","data_offsets":[0,4]}}', bytes(4), "Invalid SafeTensors tensor x in e.safetensors: missing array shape"),
+    ('{"x":{"dtype":"F32","shape":[1]}}', bytes(4), "missing array data_offsets"),
+    ('{"x":{"dtype":"F32","shape":["1"],"data_offsets":[0,4]}}', bytes(4), "Invalid SafeTensors tensor x in e.safetensors: non-integer shape"),
+    ('{"x":{"dtype":"F32","shape":[1],"data_offsets":[0,true]}}', bytes(4), "non-integer data_offsets"),
+    ('{"x":{"dtype":"F32","shape":[1],"data_offsets":[0,4,8]}}', bytes(8), "Invalid SafeTensors data_offsets for x in e.safetensors"),
+    ('{"x":{"dtype":"F32","shape":[1],"data_offsets":[-4,0]}}', bytes(4), r"Invalid SafeTensors data range for x: \[-4, 0\]"),
+    ('{"x":{"dtype":"F32","shape":[1],"data_offsets":[8,4]}}', bytes(8), r"Invalid SafeTensors data range for x: \[8, 4\]"),
+    ('{"x":{"dtype":"F32","shape":[1],"data_offsets":[0,8]}}', bytes(4),
+     r"SafeTensors data range for x escapes file bounds: \[0, 8\] fileSize="),
+    ('{"x":{"dtype":"F32","shape":[-1],"data_offsets":[0,4]}}', bytes(4),
+     "Invalid negative dimension for SafeTensors tensor x in e.safetensors: -1"),
+    ('{"x":{"dtype":"Q4","shape":[1],"data_offsets":[0,4]}}', bytes(4), "Unsupported SafeTensors dtype: Q4"),
+    ('{"x":{"dtype":"F32","shape":[1],"data_offsets":[0,4]}', bytes(4), "Invalid SafeTensors header JSON"),
+])
+def test_safetensors_entry_errors(tmp_path, header, tail, match):
+    _err(wf.write_safetensors(tmp_path / "e.safetensors", [], header=header, tail=tail), match)
+
+
+def test_safetensors_container_errors(tmp_path):
+    small = tmp_path / "s.safetensors"
+    small.write_bytes(b"\x01\x02\x03")
+    _err(small, "Invalid SafeTensors file: too small: " + str(small))
+    for hl, name in ((1, "h1"), (100, "h2"), (-5, "h3")):
+        p = tmp_path / (name + ".safetensors")
+        p.write_bytes(struct.pack("<q", hl) + b"{}" + bytes(4))
+        _err(p, "Invalid SafeTensors header length for %s.safetensors: %d" % (name, hl))
+
+
+def test_dense_tensor_quantize_checks_before_any_device_work(tmp_path):
+    """mnb_pack_weight_quantize reads and checks the dense matrix on the host
+    first: an unknown name, a shape other than the expected [rows, cols]
+    (Qwen2Weights.validateMatrixShape's text) and a BF16 tensor (which the
+    reference's embedding table refuses) fail with MNB_ERR_IO before the
+    context is used; a good tensor then needs a context."""
+    import ctypes
+    L = mnb_hip.load()
+    p = wf.write_safetensors(tmp_path / "model.safetensors",
+                             [("model.embed_tokens.weight", "F32", (6, 32), bytes(6 * 32 * 4)),
+                              ("b", "BF16", (6, 32), bytes(6 * 32 * 2))])
+    with Pack(p) as pk:
+        h = ctypes.c_void_p()
+        cases = [(b"nope", 6, 32, mnb_hip.MNB_ERR_IO, "Tensor not found: nope"),
+                 (b"model.embed_tokens.weight", 7, 32, mnb_hip.MNB_ERR_IO,
+                  "Unexpected dimensions for model.embed_tokens.weight: [6, 32], expected [7, 32]"),
+                 (b"b", 6, 32, mnb_hip.MNB_ERR_IO, "Unsupported inline tensor data for b: BFLOAT16 (16)"),
+                 (b"model.embed_tokens.weight", 6, 32, mnb_hip.MNB_ERR_INVALID_STATE, "Kernel not prepared")]
+        for name, r, c, code, msg in cases:
+            rc = L.mnb_pack_weight_quantize(None, pk.handle, name, r, c, 0, ctypes.byref(h))
+            assert rc == code and msg in mnb_hip.last_error(), (name, rc, mnb_hip.last_error())

@@ -230,3 +230,26 @@ class OnnxBuilder:
             with open(os.path.join(directory, data_name), "wb") as f:
                 f.write(bytes(self.ext))
         return path
+
+
+# ---------------------------------------------------------------------------
+# SafeTensors files (the container SafeTensorsReader.java:84-277 reads)
+# ---------------------------------------------------------------------------
+
+def write_safetensors(path, tensors, metadata=None, header=None, tail=b""):
+    """tensors: list of (name, dtype str, shape, payload bytes) laid out in
+    order; `header` (a str) replaces the generated JSON directory."""
+    import json as _json
+    import struct as _struct
+    directory, blobs, off = {}, [], 0
+    for name, dtype, shape, data in tensors:
+        directory[name] = {"dtype": dtype, "shape": list(shape), "data_offsets": [off, off + len(data)]}
+        blobs.append(data)
+        off += len(data)
+    if metadata is not None:
+        directory["__metadata__"] = metadata
+    text = header if header is not None else _json.dumps(directory)
+    hb = text.encode("utf-8")
+    with open(path, "wb") as f:
+        f.write(_struct.pack("<q", len(hb)) + hb + b"".join(blobs) + tail)
+    return str(path)

@@ -36,17 +36,22 @@
 //   workgroups is written as fp32 partial tiles, one per contributor, and
 //   summed in contributor order by sk_reduce_kernel, launched right after on
 //   the same stream over the whole chip; no workgroup ever waits for another.
-// - Tile list (groups with several tiles per workgroup): a host-built list
-//   (mnb_sched.cpp) gives each workgroup whole tiles, ordered so that the
-//   workgroups of one XCD run tiles sharing x rows and weight columns side by
-//   side; no tile is split.  These launches may use 512-column tiles (8 waves
-//   of 128 x 64, a two-slot ring), which halve the LDS reads of x per MFMA,
-//   and stage whole fp16 output tiles through LDS so that each store writes
-//   16 rows x 64 bytes; for groups whose M is at most 32 (down to M = 2),
-//   32 x 512 tiles (one 32-row fragment per wave, a three-slot ring): then
-//   the kernel is a weight stream whose x rows are shared in LDS; and for
-//   groups whose M is at most 64, 64 x 512 tiles (two 32-row fragments per
-//   wave, a three-slot ring), half the MFMA work of 128-row tiles.
+// - Tile list (groups with several tiles per workgroup, and single products
+//   with many tiles): a list (a host-built table, mnb_sched.cpp, or for one
+//   product the same list in closed form) gives each workgroup whole tiles,
+//   ordered so that the workgroups of one XCD run tiles sharing x rows and
+//   weight columns side by side; no tile is split.  These launches may use
+//   512-column tiles (8 waves of 128 x 64), which halve the LDS reads of x
+//   per MFMA, and stage whole fp16 output tiles through 20 KiB of LDS so that
+//   each store writes 16 rows x 64 bytes; for groups whose M is at most 32
+//   (down to M = 2), 32 x 512 tiles (one 32-row fragment per wave): then the
+//   kernel is a weight stream whose x rows are shared in LDS; and for groups
+//   whose M is at most 64, 64 x 512 tiles (two 32-row fragments per wave),
+//   half the MFMA work of 128-row tiles.  The ring has three slots where
+//   three fit the 160 KiB of LDS beside the staging (32 x 512 tiles with fp16
+//   scales at bs >= 32 or fp32 scales at bs >= 64), else two (128- and
+//   64-row 512-column tiles, and 32-row tiles with fp32 scales at bs 32 or
+//   fp16 scales at bs 16).
 // Logical workgroup ids are laid out XCD-contiguous, so neighbouring
 // workgroups (which share tiles and weight columns) sit on the same XCD.
 #include <algorithm>

@@ -138,7 +138,7 @@ struct Json {
 
 class JsonReader {
 public:
-    JsonReader(const char *p, size_t n) : b_(p), p_(p), e_(p + n) {}
+    JsonReader(const char *p, size_t n, const char *what = "wdmlpack manifest") : b_(p), p_(p), e_(p + n), what_(what) {}
 
     Json document() {
         ws();
@@ -150,9 +150,10 @@ public:
 
 private:
     const char *b_, *p_, *e_;
+    const char *what_;
 
     [[noreturn]] void err(const char *what) {
-        io_error(fmt("Invalid wdmlpack manifest JSON at byte %lld: %s", (long long)(p_ - b_), what));
+        io_error(fmt("Invalid %s JSON at byte %lld: %s", what_, (long long)(p_ - b_), what));
     }
     void ws() {
         while (p_ < e_ && (*p_ == ' ' || *p_ == '\t' || *p_ == '\n' || *p_ == '\r')) ++p_;
@@ -488,7 +489,8 @@ struct Pb {
     }
 };
 
-constexpr int32_t kOnnxFloat = 1, kOnnxUint8 = 2, kOnnxInt8 = 3, kOnnxInt32 = 6, kOnnxInt64 = 7, kOnnxFloat16 = 10;
+constexpr int32_t kOnnxFloat = 1, kOnnxUint8 = 2, kOnnxInt8 = 3, kOnnxInt32 = 6, kOnnxInt64 = 7, kOnnxFloat16 = 10,
+                  kOnnxBfloat16 = 16;
 
 const char *onnx_type_name(int32_t t) {  // Q2W:2133-2143
     switch (t) {
@@ -498,6 +500,7 @@ const char *onnx_type_name(int32_t t) {  // Q2W:2133-2143
     case kOnnxInt8: return "INT8";
     case kOnnxInt32: return "INT32";
     case kOnnxInt64: return "INT64";
+    case kOnnxBfloat16: return "BFLOAT16";
     default: return "UNKNOWN";
     }
 }
@@ -1296,6 +1299,116 @@ void open_wdmlpack(mnb_pack &pk) {
              " (this loader reads architecture phi3 and model.architecture qwen2): " + pk.file->path);
 }
 
+// --- SafeTensors container (SafeTensorsReader.java:84-277) -----------------
+// An 8-byte little-endian header length, a JSON directory {name: {dtype,
+// shape, data_offsets}, "__metadata__": ...}, then the tensor bytes.  The
+// reference checks each entry in this order and with these messages.
+int32_t st_bytes_per_element(const std::string &dt) {  // SafeTensorsReader.java:248-256
+    if (dt == "F16" || dt == "BF16" || dt == "I16" || dt == "U16") return 2;
+    if (dt == "F32" || dt == "I32" || dt == "U32") return 4;
+    if (dt == "F64" || dt == "I64" || dt == "U64") return 8;
+    if (dt == "I8" || dt == "U8" || dt == "BOOL") return 1;
+    io_error("Unsupported SafeTensors dtype: " + dt);
+}
+
+int32_t st_onnx_type(const std::string &dt) {  // SafeTensorsReader.java:258-276
+    static const std::pair<const char *, int32_t> kTypes[] = {
+        {"F32", 1}, {"U8", 2}, {"I8", 3}, {"I32", 6}, {"I64", 7}, {"F16", 10}, {"BF16", 16},
+        {"BOOL", 9}, {"F64", 11}, {"I16", 5}, {"U16", 4}, {"U32", 12}, {"U64", 13}};
+    for (const auto &t : kTypes)
+        if (dt == t.first) return t.second;
+    io_error("Unsupported SafeTensors dtype: " + dt);
+}
+
+std::string base_name(const std::string &p) {
+    const size_t s = p.find_last_of('/');
+    return s == std::string::npos ? p : p.substr(s + 1);
+}
+
+// Jackson's canConvertToLong: integers that fit 64 bits, and reals inside the
+// long range (converted by truncation, as asLong does).
+bool st_long_array(const Json *v, std::vector<int64_t> &out) {
+    out.clear();
+    for (const Json &e : v->a) {
+        if (e.kind == Json::Int) {
+            out.push_back(e.i);
+        } else if (e.kind == Json::Real && e.d >= -9223372036854775808.0 && e.d <= 9223372036854775807.0) {
+            out.push_back(java_d2l(e.d));
+        } else {
+            return false;
+        }
+    }
+    return true;
+}
+
+void open_safetensors(mnb_pack &pk) {
+    const MappedFile &f = *pk.file;
+    const std::string fname = base_name(f.path);
+    if (f.size < 8) io_error("Invalid SafeTensors file: too small: " + f.path);
+    const int64_t hlen = le<int64_t>(f.data);
+    if (hlen < 2 || hlen > f.size - 8) io_error(fmt("Invalid SafeTensors header length for %s: %lld", fname.c_str(), (long long)hlen));
+    if (8 + hlen > 2147483647LL) io_error(fmt("SafeTensors header too large for current reader: %lld", (long long)hlen));
+    const Json root = JsonReader((const char *)f.data + 8, (size_t)hlen, "SafeTensors header").document();
+    const int64_t base = 8 + hlen;
+    pk.kind = MNB_PACK_SAFETENSORS;
+    if (root.kind != Json::Obj) return;   // a directory that is not an object lists no tensors
+    // members in file order; a repeated name keeps its first position and its last value
+    std::vector<std::string> order;
+    std::unordered_map<std::string, const Json *> entry;
+    for (const auto &m : root.o) {
+        if (!entry.count(m.first)) order.push_back(m.first);
+        entry[m.first] = &m.second;
+    }
+    for (const std::string &name : order) {
+        if (name == "__metadata__") continue;
+        const Json &node = *entry[name];
+        if (node.kind != Json::Obj) io_error("Invalid SafeTensors tensor entry for " + name + " in " + fname);
+        const Json *dt = node.get("dtype");
+        if (!dt || dt->kind != Json::Str)
+            io_error("Invalid SafeTensors tensor " + name + " in " + fname + ": missing textual dtype");
+        std::string dtype = dt->s;
+        for (char &c : dtype) c = (char)toupper((unsigned char)c);
+        std::vector<int64_t> shape, offsets;
+        for (const char *field : {"shape", "data_offsets"}) {
+            const Json *v = node.get(field);
+            if (!v || v->kind != Json::Arr)
+                io_error("Invalid SafeTensors tensor " + name + " in " + fname + ": missing array " + field);
+            if (!st_long_array(v, strcmp(field, "shape") == 0 ? shape : offsets))
+                io_error("Invalid SafeTensors tensor " + name + " in " + fname + ": non-integer " + field);
+        }
+        if (offsets.size() != 2) io_error("Invalid SafeTensors data_offsets for " + name + " in " + fname);
+        const int64_t begin = offsets[0], end = offsets[1];
+        if (begin < 0 || end < begin)
+            io_error(fmt("Invalid SafeTensors data range for %s: [%lld, %lld]", name.c_str(), (long long)begin,
+                         (long long)end));
+        int64_t abs_begin = 0, abs_end = 0;
+        if (__builtin_add_overflow(base, begin, &abs_begin) || __builtin_add_overflow(base, end, &abs_end) ||
+            abs_end > f.size)
+            io_error(fmt("SafeTensors data range for %s escapes file bounds: [%lld, %lld] fileSize=%lld", name.c_str(),
+                         (long long)begin, (long long)end, (long long)f.size));
+        int64_t elements = 1;
+        for (int64_t d : shape) {
+            if (d < 0)
+                io_error(fmt("Invalid negative dimension for SafeTensors tensor %s in %s: %lld", name.c_str(),
+                             fname.c_str(), (long long)d));
+            if (__builtin_mul_overflow(elements, d, &elements)) io_error("long overflow");
+        }
+        int64_t expected = 0;
+        if (__builtin_mul_overflow(elements, (int64_t)st_bytes_per_element(dtype), &expected)) io_error("long overflow");
+        if (expected != end - begin)
+            io_error(fmt("SafeTensors byte length mismatch for %s in %s: expected %lld bytes from dtype/shape, got %lld",
+                         name.c_str(), fname.c_str(), (long long)expected, (long long)(end - begin)));
+        Tensor t;
+        t.name = name;
+        t.dtype = st_onnx_type(dtype);
+        t.dims = shape;
+        t.raw = f.data + abs_begin;
+        t.raw_len = end - begin;
+        pk.names.push_back(name);
+        pk.inline_tensors[name] = std::move(t);
+    }
+}
+
 // Runs one entry point's body: IoError -> MNB_ERR_IO with its text, host
 // allocation failure -> MNB_ERR_OUT_OF_MEMORY.
 template <class F>
@@ -1330,10 +1443,16 @@ int32_t mnb_pack_open(const char *path, mnb_pack **out) {
     return guarded([&] {
         std::unique_ptr<mnb_pack> pk(new mnb_pack());
         pk->file.reset(new MappedFile(path));
-        const std::string p(path), ext = ".wdmlpack";
-        const bool named = p.size() >= ext.size() && p.compare(p.size() - ext.size(), ext.size(), ext) == 0;
-        if (named || (pk->file->size >= 8 && memcmp(pk->file->data, "WDMLPACK", 8) == 0)) open_wdmlpack(*pk);
-        else open_onnx(*pk);
+        const std::string p(path);
+        auto ends_with = [&](const std::string &ext) {
+            return p.size() >= ext.size() && p.compare(p.size() - ext.size(), ext.size(), ext) == 0;
+        };
+        if (ends_with(".wdmlpack") || (pk->file->size >= 8 && memcmp(pk->file->data, "WDMLPACK", 8) == 0))
+            open_wdmlpack(*pk);
+        else if (ends_with(".safetensors"))
+            open_safetensors(*pk);
+        else
+            open_onnx(*pk);
         *out = pk.release();
         return MNB_OK;
     });
@@ -1368,9 +1487,11 @@ int32_t mnb_pack_find_projection(const mnb_pack *pack, int32_t layer, const char
                                  int64_t *length) {
     if (!pack || !projection) return mnb::report(MNB_ERR_INVALID_ARGUMENT, "pack and projection must not be null");
     const std::string prefix = "layers." + std::to_string(layer);
-    for (const std::string &n : pack->names)
+    for (const std::string &n : pack->names) {
+        if (pack->kind == MNB_PACK_SAFETENSORS) break;   // dense tensors only: no quantized weights
         if (n.find(prefix) != std::string::npos && n.find(projection) != std::string::npos)
             return copy_name(n, buf, cap, length);
+    }
     return mnb::report(MNB_ERR_IO, fmt("Quantized weight not found for layer %d %s", layer, projection).c_str());
 }
 
@@ -1409,6 +1530,58 @@ int32_t mnb_pack_read_weight(const mnb_pack *pack, const char *name, uint8_t *q,
         if (zb > 0) memcpy(zp, t.zp, (size_t)zb);
         return MNB_OK;
     });
+}
+
+int32_t mnb_pack_tensor_info(const mnb_pack *pack, const char *name, int32_t *dtype, int64_t *dims, int32_t dims_cap,
+                             int32_t *ndims) {
+    if (!pack || !name || !dtype || !ndims)
+        return mnb::report(MNB_ERR_INVALID_ARGUMENT, "pack, name, dtype and ndims must not be null");
+    return guarded([&] {
+        const Tensor *t = pack->find_ext(name);
+        if (!t) t = pack->find_inline(name);
+        if (!t) {
+            auto it = pack->tensors.find(name);
+            if (it != pack->tensors.end()) t = &it->second;
+        }
+        if (!t) io_error(std::string("Tensor not found: ") + name);
+        *dtype = t->dtype;
+        *ndims = (int32_t)t->dims.size();
+        for (int32_t i = 0; i < *ndims && i < dims_cap && dims; ++i) dims[i] = t->dims[(size_t)i];
+        return MNB_OK;
+    });
+}
+
+int32_t mnb_pack_weight_quantize(mnb_context *ctx, const mnb_pack *pack, const char *name, int32_t rows, int32_t cols,
+                                 int32_t block_size, mnb_weight **out) {
+    if (!out) return mnb::report(MNB_ERR_INVALID_ARGUMENT, "out must not be null");
+    *out = nullptr;
+    if (!pack || !name) return mnb::report(MNB_ERR_INVALID_ARGUMENT, "pack and name must not be null");
+    std::vector<float> data;
+    const int32_t rr = guarded([&] {
+        const Tensor *t = pack->find_ext(name);
+        if (!t) t = pack->find_inline(name);
+        if (!t) io_error(std::string("Tensor not found: ") + name);
+        // Qwen2Weights.validateMatrixShape (Q2W:1637-1642)
+        if (!(t->dims.size() == 2 && t->dims[0] == rows && t->dims[1] == cols)) {
+            std::string d = "[";
+            for (size_t i = 0; i < t->dims.size(); ++i) d += (i ? ", " : "") + std::to_string(t->dims[i]);
+            io_error(fmt("Unexpected dimensions for %s: %s], expected [%d, %d]", name, d.c_str(), rows, cols));
+        }
+        // the embedding table's values: FLOAT as stored, FLOAT16 through the
+        // reference's fp16ToFp32 (Q2W:200-270, 599-704); other types refused
+        int32_t dt = 0;
+        if (!resolve_float(*pack, name, data, dt)) io_error(std::string("Tensor has no data: ") + name);
+        if ((int64_t)data.size() != (int64_t)rows * cols)
+            io_error(fmt("Tensor %s holds %zu values, expected %lld", name, data.size(), (long long)rows * cols));
+        return MNB_OK;
+    });
+    if (rr != MNB_OK) return rr;
+    const int32_t rc = mnb_weight_quantize(ctx, data.data(), MNB_F32, rows, cols, block_size, MNB_HOST_MEMORY, out);
+    if (rc != MNB_OK) {
+        const std::string msg = std::string(name) + ": " + mnb_last_error();
+        return mnb::report(rc, msg.c_str());
+    }
+    return MNB_OK;
 }
 
 int32_t mnb_pack_weight_create(mnb_context *ctx, const mnb_pack *pack, const char *name, mnb_weight **out) {

@@ -46,7 +46,7 @@ MNB_ZP_ROW_PADDED = 2
 MNB_HOST_MEMORY = 0x1
 MNB_ACCUMULATE = 0x2
 MNB_COPY_H2D, MNB_COPY_D2H, MNB_COPY_D2D = 0, 1, 2
-MNB_PACK_PHI3, MNB_PACK_QWEN2, MNB_PACK_ONNX = 1, 2, 3
+MNB_PACK_PHI3, MNB_PACK_QWEN2, MNB_PACK_ONNX, MNB_PACK_SAFETENSORS = 1, 2, 3, 4
 
 # Every symbol include/mnb.h declares.
 EXPORTED_SYMBOLS = (
@@ -56,6 +56,7 @@ EXPORTED_SYMBOLS = (
     "mnb_memcpy", "mnb_synchronize", "mnb_group_create", "mnb_group_run", "mnb_group_destroy", "mnb_matmul_plan", "mnb_group_plan",
     "mnb_pack_open", "mnb_pack_close", "mnb_pack_kind", "mnb_pack_weight_count", "mnb_pack_weight_name",
     "mnb_pack_find_projection", "mnb_pack_weight_info", "mnb_pack_read_weight", "mnb_pack_weight_create",
+    "mnb_pack_tensor_info", "mnb_pack_weight_quantize",
 )
 
 
@@ -174,6 +175,9 @@ def load() -> ctypes.CDLL:
         "mnb_pack_weight_info": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(TripletInfo)]),
         "mnb_pack_read_weight": (i32, [vp, ctypes.c_char_p, vp, i64, vp, i64, vp, i64]),
         "mnb_pack_weight_create": (i32, [vp, vp, ctypes.c_char_p, ctypes.POINTER(vp)]),
+        "mnb_pack_tensor_info": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(i32), ctypes.POINTER(i64), i32,
+                                       ctypes.POINTER(i32)]),
+        "mnb_pack_weight_quantize": (i32, [vp, vp, ctypes.c_char_p, i32, i32, i32, ctypes.POINTER(vp)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -583,6 +587,21 @@ class Pack:
         check(load().mnb_pack_read_weight(self.handle, _name_bytes(name), q.ctypes.data, q.size, s.ctypes.data, s.size,
                                           z.ctypes.data if z.size else None, z.size))
         return q, s, z
+
+    def tensor_info(self, name: str):
+        """(ONNX element type, shape) of any tensor of the file (mnb_pack_tensor_info)."""
+        dt, nd = ctypes.c_int32(), ctypes.c_int32()
+        dims = (ctypes.c_int64 * 16)()
+        check(load().mnb_pack_tensor_info(self.handle, _name_bytes(name), ctypes.byref(dt), dims, 16, ctypes.byref(nd)))
+        return dt.value, tuple(dims[i] for i in range(min(nd.value, 16)))
+
+    def quantize(self, ctx: Context, name: str, rows: int, cols: int, block_size: int = 0) -> Weight:
+        """Dense [rows, cols] tensor -> int4 weight on the device (mnb_pack_weight_quantize): the
+        reference's runtime-quantized tied lm_head read from the file."""
+        h = ctypes.c_void_p()
+        check(load().mnb_pack_weight_quantize(ctx.handle, self.handle, _name_bytes(name), rows, cols, block_size,
+                                              ctypes.byref(h)), "prepare")
+        return Weight._adopt(ctx, h)
 
     def weight(self, ctx: Context, name: str) -> Weight:
         """Upload one triplet to HBM (mnb_pack_weight_create)."""
