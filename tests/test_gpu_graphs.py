@@ -5,8 +5,9 @@ and the batched recording of WarpExecutionContext.java:131-160).
 
 Products on device pointers allocate nothing and record only kernel launches,
 so a sequence of them -- single-row products, a prefill product whose tiles
-are split over workgroups (GEMM plus its reduce kernel), and a group launch --
-is captured into a HIP graph on a fresh context, with no eager call first.
+are split over workgroups (GEMM plus its reduce kernel), a prefill product
+on the K-sliced kernel, and a group launch -- is captured into a HIP graph on
+a fresh context, with no eager call first.
 Each replay, with new activations written by eager work between replays,
 equals the eager calls bit for bit."""
 import numpy as np
@@ -32,21 +33,27 @@ def test_graph_capture_replays_match_eager():
         dev = "cuda"
         w_o = _weight(ctx, 1, 3072, 3072)                  # decode o_proj
         w_gu = _weight(ctx, 2, 16384, 3072)                # decode gate_up
-        w_pf = _weight(ctx, 3, 1000, 3072, zp=True)        # prefill product with split tiles
+        w_pf = _weight(ctx, 3, 9001, 8192, zp=True)        # prefill product with split tiles
+        w_ks = _weight(ctx, 4, 1000, 3072, zp=True)        # prefill product on the K-sliced kernel
+        assert w_pf.plan(200).as_tuple() == (mnb_hip.MNB_KERNEL_GEMM, mnb_hip.MNB_ORDER_STREAM_K, 128, 256)
+        assert w_ks.plan(200).kernel == mnb_hip.MNB_KERNEL_KSLICE
         w_g = [_weight(ctx, 10 + i, 1536, 576, 64, zp=True) for i in range(3)]
         gen = torch.Generator(device=dev).manual_seed(7)
         x1 = torch.empty(3072, device=dev, dtype=torch.float16)
-        xp = torch.empty(200, 3072, device=dev, dtype=torch.float16)
+        xp = torch.empty(200, 8192, device=dev, dtype=torch.float16)
+        xk = torch.empty(200, 3072, device=dev, dtype=torch.float16)
         xg = [torch.empty(576, device=dev, dtype=torch.float16) for _ in w_g]
         y_o = torch.empty(3072, device=dev, dtype=torch.float16)
         y_gu = torch.empty(16384, device=dev, dtype=torch.float32)
-        y_pf = torch.empty(200, 1000, device=dev, dtype=torch.float16)
+        y_pf = torch.empty(200, 9001, device=dev, dtype=torch.float16)
+        y_ks = torch.empty(200, 1000, device=dev, dtype=torch.float32)
         y_g = [torch.empty(1536, device=dev, dtype=torch.float16) for _ in w_g]
         st = torch.cuda.Stream()
 
         def fill():
             x1.copy_(torch.randn(3072, device=dev, generator=gen).half())
-            xp.copy_(torch.randn(200, 3072, device=dev, generator=gen).half())
+            xp.copy_(torch.randn(200, 8192, device=dev, generator=gen).half())
+            xk.copy_(torch.randn(200, 3072, device=dev, generator=gen).half())
             for x in xg:
                 x.copy_(torch.randn(576, device=dev, generator=gen).half())
 
@@ -59,6 +66,7 @@ def test_graph_capture_replays_match_eager():
             w_o.matmul(x1, y_o, stream=st.cuda_stream)
             w_gu.matmul(x1, y_gu, stream=st.cuda_stream)
             w_pf.matmul(xp, y_pf, stream=st.cuda_stream)
+            w_ks.matmul(xk, y_ks, stream=st.cuda_stream)
             group.run(st.cuda_stream)
 
         graph = torch.cuda.CUDAGraph()
@@ -66,7 +74,7 @@ def test_graph_capture_replays_match_eager():
             record()
         torch.cuda.synchronize()
 
-        outs = [y_o, y_gu, y_pf] + y_g
+        outs = [y_o, y_gu, y_pf, y_ks] + y_g
         for rep in range(4):
             with torch.cuda.stream(st):
                 fill()
@@ -85,7 +93,7 @@ def test_graph_capture_replays_match_eager():
                 assert torch.equal(a.view(torch.int16) if a.dtype == torch.float16 else a.view(torch.int32),
                                    b.view(torch.int16) if b.dtype == torch.float16 else b.view(torch.int32)), (rep, i)
         group.close()
-        for w in [w_o, w_gu, w_pf] + w_g:
+        for w in [w_o, w_gu, w_pf, w_ks] + w_g:
             w.close()
         del graph
     finally:

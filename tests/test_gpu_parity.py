@@ -7,7 +7,7 @@ Bars (stated per test):
   plus one fp16 ulp of |y_oracle| when the output is fp16.
 * full-size shapes: the oracle on sampled output rows, and properties that
   hold bit-for-bit (power-of-two scaling, row independence of the skinny
-  kernel, run-to-run determinism of the stream-K GEMM).
+  kernel, run-to-run determinism of the GEMM and the K-sliced kernel).
 """
 import os
 import subprocess
@@ -216,12 +216,14 @@ def test_rows_are_independent_in_skinny_kernel(ctx):
 
 
 def test_gemm_determinism_tiling_and_pow2_scaling(ctx):
-    """The stream-K GEMM splits K over workgroups by the tile count, so a row's
-    summation order depends on M: rows of an M=512 product match an M=128
-    product of the same rows to the tolerance, and repeated calls with the
-    same M are bitwise identical (partials are summed in a fixed order)."""
-    t = synth.make_weight(13, 3072, 3072, 32)
+    """The schedule, and for single products the kernel, depend on M, so a
+    row's summation order depends on M: rows of an M=512 product (the GEMM)
+    match an M=128 product of the same rows (the K-sliced kernel) to the
+    tolerance, and repeated calls with the same M are bitwise identical
+    (nothing is summed in an order that depends on timing)."""
+    t = synth.make_weight(13, 9216, 3072, 32)
     w = upload(ctx, t)
+    assert w.plan(512).kernel == GEMM and w.plan(128).kernel == KSLICE, (w.plan(512).as_tuple(), w.plan(128).as_tuple())
     x16 = synth.make_x(14, 512, 3072)
     y = w.matmul(x16)
     for _ in range(3):
@@ -265,20 +267,24 @@ def test_tall_single_row_product(ctx):
         w.close()
 
 
-@pytest.mark.parametrize("M,K,N", [(200, 3072, 1000), (300, 4096, 1001), (130, 8192, 3072)])
+@pytest.mark.parametrize("M,K,N", [(200, 8192, 9001), (250, 6144, 7001), (150, 8192, 10001)])
 def test_gemm_split_tiles_tails_and_outputs(ctx, M, K, N):
-    """Few tiles, so stream-K splits them across workgroups and the partial
-    tiles go through the reduce kernel.  M and N tails (N % 4 != 0 falls back
-    to per-element stores), fp16 and fp32 outputs, y += and a y that is not
-    aligned for 4-element stores: all within the tolerance of the oracle,
-    bitwise repeatable, and y += equal to y0 + y."""
+    """Few 128 x 256 tiles for their K, so stream-K splits them across
+    workgroups and the partial tiles go through the reduce kernel (shapes
+    where the GEMM beats the K-sliced kernel).  M and N tails (N % 4 != 0
+    falls back to per-element stores), fp16 and fp32 outputs, y += and a y
+    that is not aligned for 4-element stores: within the tolerance of the
+    oracle on sampled columns, bitwise repeatable, and y += equal to y0 + y."""
     import torch
     t = synth.make_weight(50 + M, N, K, 32, with_zp=True)
     w = upload(ctx, t)
+    assert w.plan(M).as_tuple() == (GEMM, STREAM_K, 128, 256), w.plan(M).as_tuple()
     x16 = synth.make_x(51 + M, M, K)
-    y_ref, wmax = oracle_matmul(t, x16)
+    rng = np.random.default_rng(M + N)
+    cols = np.sort(np.concatenate([rng.choice(N - 16, 240, replace=False), np.arange(N - 16, N)]))
+    y_ref, _ = oracle_matmul(t, x16, cols, want_wmax=False)
     y32 = w.matmul(x16)
-    assert_parity(y32, y_ref, x16, t, wmax, False, "split f32 M=%d K=%d N=%d" % (M, K, N))
+    assert_parity(y32[:, cols], y_ref, x16, t, None, False, "split f32 M=%d K=%d N=%d" % (M, K, N))
     assert np.array_equal(w.matmul(x16).view(np.uint32), y32.view(np.uint32))
     y16 = w.matmul(x16, out_dtype=np.float16)
     assert np.array_equal(y16.view(np.uint16), y32.astype(np.float16).view(np.uint16))
@@ -294,6 +300,71 @@ def test_gemm_split_tiles_tails_and_outputs(ctx, M, K, N):
     assert np.array_equal(yd.cpu().numpy().reshape(M, N).view(np.uint32), y32.view(np.uint32))
     assert float(buf[0].item()) == 0.0
     w.close()
+
+
+@pytest.mark.parametrize("case", [
+    # M, K, N, bs, zero points, fp32 scales (not fp16-exact), output block
+    (40, 1000, 300, 32, True, False, (32, 16)),
+    (17, 3000, 1001, 32, False, True, (32, 16)),
+    (129, 576, 1000, 64, True, False, (32, 32)),
+    (48, 1536, 4000, 16, False, False, (32, 32)),
+    (300, 4096, 1001, 128, True, False, (32, 64)),
+    (130, 8192, 3072, 32, False, False, (32, 64)),
+    (64, 3072, 9216, 32, False, False, (64, 64)),
+    (250, 3072, 3070, 32, True, False, (64, 64))],
+    ids=lambda c: "M%d-K%d-N%d-bs%d%s%s" % (c[0], c[1], c[2], c[3], "-zp" if c[4] else "", "-f32s" if c[5] else ""))
+def test_single_products_k_sliced(ctx, case):
+    """Single products where the GEMM would have few tiles run on the
+    K-sliced kernel (workgroup = 16 MB rows x 16 NTW columns over the whole K,
+    its waves' K slices summed in LDS in wave order): each of its four output
+    blocks, M, N and K tails (rows past M, n-tiles past N, a partial last
+    super-tile), zero points, bs 16 to 128, fp32 scales, fp16 and fp32
+    outputs, y +=, a y not aligned for 4-column stores.  Within the tolerance
+    of the oracle, bitwise repeatable, fp16 output = fp32 output rounded, and
+    y += equal to y0 + y."""
+    import torch
+    M, K, N, bs, zp, f32s, block = case
+    t = synth.make_weight(9100 + M + N, N, K, bs, with_zp=zp)
+    if f32s:    # scales that fp16 cannot hold: the device keeps fp32 scales
+        s = t.scales_f16.astype(np.float32) * np.float32(1.0 + 2.0 ** -14)
+        w = mnb_hip.Weight(ctx, N, K, bs, t.q, s)
+    else:
+        w = upload(ctx, t)
+    try:
+        p = w.plan(M)
+        if f32s:
+            assert p.kernel == KSLICE, p.as_tuple()
+        else:
+            assert p.as_tuple() == (KSLICE, NO_ORDER) + block, p.as_tuple()
+        x16 = synth.make_x(9200 + M, M, K)
+        if f32s:
+            kb = t.kb
+            z = synth.zp_row_padded_to_flat(np.full((N, (kb + 1) // 2), 0x88, np.uint8), N, kb)
+            xp = np.zeros((M, kb * bs), np.float32)
+            xp[:, :K] = x16.astype(np.float32)
+            y_ref = orc.matmul(t.q, s, z, N, kb * bs, bs, xp, threads=THREADS)
+            wmax = float(np.abs(s).max()) * 8.0
+        else:
+            y_ref, wmax = oracle_matmul(t, x16)
+        label = "k-sliced M=%d K=%d N=%d bs=%d" % (M, K, N, bs)
+        y32 = w.matmul(x16)
+        assert_parity(y32, y_ref, x16, t, wmax, False, label)
+        assert np.array_equal(w.matmul(x16).view(np.uint32), y32.view(np.uint32))
+        y16 = w.matmul(x16, out_dtype=np.float16)
+        assert np.array_equal(y16.view(np.uint16), y32.astype(np.float16).view(np.uint16))
+        y0 = np.random.default_rng(M + K).standard_normal((M, N)).astype(np.float32)
+        acc = w.matmul(x16, y=y0.copy(), accumulate=True)
+        assert np.array_equal(acc.view(np.uint32), (y0 + y32).view(np.uint32))
+        # device output one element past an aligned address: per-element stores
+        xd = torch.from_numpy(x16).cuda()
+        buf = torch.zeros(M * N + 1, dtype=torch.float32, device="cuda")
+        yd = buf[1:]
+        w.matmul(xd, yd)
+        torch.cuda.synchronize()
+        assert np.array_equal(yd.cpu().numpy().reshape(M, N).view(np.uint32), y32.view(np.uint32))
+        assert float(buf[0].item()) == 0.0
+    finally:
+        w.close()
 
 
 def test_accumulate_and_dtypes_and_zp_layouts(ctx):
@@ -430,7 +501,7 @@ def test_group_matches_oracle_and_single_launches(ctx):
         w.close()
 
 
-GEMM, GEMV_GROUP = mnb_hip.MNB_KERNEL_GEMM, mnb_hip.MNB_KERNEL_GEMV_GROUP
+GEMM, GEMV_GROUP, KSLICE = mnb_hip.MNB_KERNEL_GEMM, mnb_hip.MNB_KERNEL_GEMV_GROUP, mnb_hip.MNB_KERNEL_KSLICE
 STREAM_K, TILE_LIST, NO_ORDER = mnb_hip.MNB_ORDER_STREAM_K, mnb_hip.MNB_ORDER_TILE_LIST, mnb_hip.MNB_ORDER_NONE
 
 
@@ -703,7 +774,7 @@ def test_tiny_block_scales_keep_the_bound(ctx, lo, hi):
 def test_single_products_with_a_k_tail_not_a_multiple_of_8(ctx, K):
     """K % 8 != 0: the kernels read x in 16-byte pieces, so x is first copied
     to fp16 rows padded to a multiple of 8 with zeros (host arrays, and device
-    fp16 or fp32 x alike); M = 1, 7 (GEMV) and 40, 200 (GEMM, split tiles),
+    fp16 or fp32 x alike); M = 1, 7 (GEMV) and 40, 200 (the K-sliced kernel),
     zero points, bs 32 and 64."""
     import torch
     for bs in (32, 64):
@@ -782,13 +853,21 @@ def test_single_products_in_closed_form_tile_order(ctx, case):
 
 
 def test_matmul_plan_reports_the_single_product_schedule(ctx):
-    """mnb_matmul_plan: the GEMV kernel up to M = 16, stream-K 128 x 256 tiles
-    for products with few tiles, closed-form 128 x 512 tile lists for
-    products with many (the Phi-3 lm_head at M = 512 and gate_up at 2048)."""
+    """mnb_matmul_plan: the GEMV kernel up to M = 16; the K-sliced kernel
+    where the GEMM would have few tiles for the chip (o_proj and down at M
+    32 to 512, qkv at 32 and 64: 32 x 16 up to 64 x 64 output blocks);
+    stream-K 128 x 256 tiles for the qkv shape at M = 512; closed-form
+    128 x 512 tile lists for products with many tiles (the Phi-3 lm_head at
+    M = 512 and gate_up at 2048)."""
     for (K, N, M), expect in [((3072, 9216, 1), (mnb_hip.MNB_KERNEL_GEMV, NO_ORDER, 0, 16)),
                               ((3072, 9216, 16), (mnb_hip.MNB_KERNEL_GEMV, NO_ORDER, 0, 16)),
-                              ((3072, 3072, 512), (GEMM, STREAM_K, 128, 256)),
-                              ((8192, 3072, 128), (GEMM, STREAM_K, 128, 256)),
+                              ((3072, 3072, 32), (KSLICE, NO_ORDER, 32, 16)),
+                              ((3072, 3072, 64), (KSLICE, NO_ORDER, 32, 32)),
+                              ((3072, 9216, 32), (KSLICE, NO_ORDER, 32, 64)),
+                              ((3072, 9216, 64), (KSLICE, NO_ORDER, 64, 64)),
+                              ((8192, 3072, 128), (KSLICE, NO_ORDER, 32, 64)),
+                              ((3072, 3072, 512), (KSLICE, NO_ORDER, 64, 64)),
+                              ((3072, 9216, 512), (GEMM, STREAM_K, 128, 256)),
                               ((3072, 32064, 512), (GEMM, TILE_LIST, 128, 512)),
                               ((3072, 16384, 2048), (GEMM, TILE_LIST, 128, 512))]:
         t = synth.make_weight(1, N, K, 32)

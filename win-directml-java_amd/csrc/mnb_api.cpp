@@ -596,7 +596,16 @@ int32_t mnb_matmul_plan(const mnb_context *ctx, const mnb_weight *w, int32_t M, 
     const int32_t ldx = (g.K + 7) & ~7;
     const int64_t chunk_rows = std::max<int64_t>(128, (((int64_t)1 << 31) / ((int64_t)ldx * 2)) / 128 * 128);
     const int32_t Mc = (int32_t)std::min<int64_t>(M, chunk_rows);
-    const mnb::SinglePlan p = mnb::sk_single_plan(Mc, g.NT, g.ST, g.scale_f32, g.SPS, ctx->cu_count);
+    const mnb::ProductPlan pp = mnb::product_plan(g, Mc, ctx->cu_count);
+    if (pp.ks) {
+        out->kernel = MNB_KERNEL_KSLICE;
+        out->order = MNB_ORDER_NONE;
+        out->tile_rows = 16 * pp.kc.mb;
+        out->tile_cols = 16 * pp.kc.ntw;
+        out->workgroups = (int32_t)mnb::ks_workgroups(Mc, g.NT, pp.kc);
+        return ok();
+    }
+    const mnb::SinglePlan &p = pp.sp;
     out->kernel = MNB_KERNEL_GEMM;
     out->order = p.closed ? MNB_ORDER_TILE_LIST : MNB_ORDER_STREAM_K;
     out->tile_rows = 32 * p.fm;
@@ -609,12 +618,22 @@ int32_t mnb_max_batch_rows(void) { return std::numeric_limits<int32_t>::max() / 
 
 }  // extern "C"
 
-// M > 16: stream-K GEMM over one persistent workgroup per CU.  ws holds the
-// partial tiles of split tiles (sk_workspace_bytes(cu_count) bytes: the
-// context's workspace, allocated with it, or the fixed scratch array of
-// mnb_matmul_noalloc).  The kernel addresses x and the weights with 32-bit
-// byte offsets: rows of x go in chunks of at most 2 GiB, and packed weights of
-// 4 GiB or more are refused.
+mnb::ProductPlan mnb::product_plan(const WeightGeom &g, int32_t M, int32_t cu_count) {
+    ProductPlan p;
+    p.sp = sk_single_plan(M, g.NT, g.ST, g.scale_f32, g.SPS, cu_count);
+    const KsPlan k = ks_single_plan(M, g.NT, g.ST, g.scale_f32, g.has_zp, g.SPS, cu_count);
+    p.ks = k.wgs > 0 && k.est < p.sp.est;
+    p.kc = k.c;
+    return p;
+}
+
+// M > 16: per chunk of rows, the K-sliced kernel or the GEMM (stream-K over
+// one persistent workgroup per CU, or a closed-form tile list), whichever the
+// cost models expect to finish first.  ws holds the GEMM's partial tiles of
+// split tiles (sk_workspace_bytes(cu_count) bytes: the context's workspace,
+// allocated with it, or the fixed scratch array of mnb_matmul_noalloc).  The
+// kernels address x and the scales with 32-bit byte offsets: rows of x go in
+// chunks of at most 2 GiB, and packed weights of 4 GiB or more are refused.
 static hipError_t launch_prefill(const mnb_weight *w, int cu_count, const mnb::MatmulArgs &a, float *ws,
                                  hipStream_t s) {
     const mnb::WeightGeom &g = w->g;
@@ -627,9 +646,11 @@ static hipError_t launch_prefill(const mnb_weight *w, int cu_count, const mnb::M
         c.M = std::min(chunk, a.M - m0);
         c.x = a.x + (size_t)m0 * a.ldx;
         c.y = (unsigned char *)a.y + (size_t)m0 * y_row;
-        const mnb::SinglePlan plan = mnb::sk_single_plan(c.M, g.NT, g.ST, g.scale_f32, g.SPS, cu_count);
-        const hipError_t e = plan.closed ? mnb::launch_gemm_closed(w, c, plan.ntw, plan.fm, plan.G, s)
-                                         : mnb::launch_gemm_sk(w, c, plan.G, ws, s);
+        const mnb::ProductPlan pp = mnb::product_plan(g, c.M, cu_count);
+        const mnb::SinglePlan &plan = pp.sp;
+        const hipError_t e = pp.ks       ? mnb::launch_gemm_ks(w, c, pp.kc, s)
+                             : plan.closed ? mnb::launch_gemm_closed(w, c, plan.ntw, plan.fm, plan.G, s)
+                                           : mnb::launch_gemm_sk(w, c, plan.G, ws, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -120,6 +120,30 @@ __device__ __forceinline__ void store_y(void *y, size_t idx, float v, bool accum
     }
 }
 
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// A wave-uniform pointer held in scalar registers.  The builtin returns a
+// signed int: each half goes back through uint32_t, so the low dword is
+// zero-extended (a sign extension would set the high dword to all ones
+// whenever bit 31 of the address is set).
+__device__ __forceinline__ const void *uniform_ptr(const void *p) {
+    const uint64_t b = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+    return (const void *)(uintptr_t)((uint64_t)lo | ((uint64_t)hi << 32));
+}
+
+// One direct global->LDS load of 16 bytes per active lane from base + off
+// (scalar base, 32-bit lane offset): lane l writes LDS[m0 + 16 l].  Issued as
+// inline asm, so the compiler neither tracks it nor moves memory accesses
+// across it; the kernel waits for it explicitly.
+__device__ __forceinline__ void dma16(uint32_t m0, uint32_t off, const void *base) {
+    asm volatile("global_load_lds_dwordx4 %1, %2" ::"{m0}"(m0), "v"(off), "s"(uniform_ptr(base)) : "memory");
+}
+
 // Load the SPS scales of one row of one tile (SPS * sizeof(ScaleT) bytes,
 // naturally aligned in the tiled layout) with the widest vector load.
 template <typename ScaleT, int SPS>

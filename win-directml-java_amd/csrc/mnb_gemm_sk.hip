@@ -238,27 +238,6 @@ __device__ __forceinline__ void store_y4(const SkItem &p, int m, int n, float4_t
     }
 }
 
-// LDS byte address of a pointer into a __shared__ array.
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-
-// One direct global->LDS load of 16 bytes per active lane from base + off
-// (scalar base, 32-bit lane offset): lane l writes LDS[m0 + 16 l].  Issued as
-// inline asm, so the compiler neither tracks it nor moves memory accesses
-// across it; the kernel waits for it explicitly.
-__device__ __forceinline__ void dma16(uint32_t m0, uint32_t off, const void *base) {
-    // the base is wave-uniform (it comes from the item tables); make that
-    // explicit so it is held in scalar registers.  The builtin returns a
-    // signed int: each half goes back through uint32_t, so the low dword is
-    // zero-extended (a sign extension would set the high dword to all ones
-    // whenever bit 31 of the address is set).
-    const uint64_t b = (uint64_t)(uintptr_t)base;
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
-    const uint64_t u = (uint64_t)lo | ((uint64_t)hi << 32);
-    asm volatile("global_load_lds_dwordx4 %1, %2" ::"{m0}"(m0), "v"(off), "s"((const void *)(uintptr_t)u) : "memory");
-}
 
 // Ring slot layout (bytes) for one stage, and the direct loads that fill it.
 template <typename ScaleT, bool HAS_ZP, int SPS, int NTW, int FM>
@@ -865,16 +844,17 @@ int sk_grid(int T, int ST, int cu_count) {
 
 SinglePlan sk_single_plan(int M, int NT, int ST, int scale_f32, int sps, int cu_count) {
     const int T = sk_tiles(M, NT);
-    SinglePlan plan{false, kSkNTW, kSkFM, sk_grid(T, ST, cu_count)};
-    if (!sk_wide_supported(scale_f32, sps)) return plan;
+    SinglePlan plan{false, kSkNTW, kSkFM, sk_grid(T, ST, cu_count), 0.0};
     const double stream_k = sk_cost(T, ST, plan.G, cu_count);
+    plan.est = stream_k;
+    if (!sk_wide_supported(scale_f32, sps)) return plan;
     const int Tw = sk_tiles(M, NT, kSkWideNTW, kSkFM);
     const int Gw = std::min(std::min(cu_count, kSkReduceThreads), Tw);
     int busiest = 0;   // tiles of the busiest workgroup in closed-form order
     for (int g = 0; g < Gw; ++g) busiest = std::max(busiest, sk_cf_first(Tw, Gw, g + 1) - sk_cf_first(Tw, Gw, g));
     const double load = (double)Gw / cu_count;
     const double wide = busiest * (ST * (1.16 + 0.38 * load) * kGemmWideStageCost + 8.6);
-    if (wide < stream_k) plan = SinglePlan{true, kSkWideNTW, kSkFM, Gw};
+    if (wide < stream_k) plan = SinglePlan{true, kSkWideNTW, kSkFM, Gw, wide};
     return plan;
 }
 

@@ -95,7 +95,7 @@ class TripletInfo(ctypes.Structure):
                 ("zp_bytes", ctypes.c_int64), ("zp_implicit", ctypes.c_int32), ("scale_dtype", ctypes.c_int32)]
 
 
-MNB_KERNEL_GEMV, MNB_KERNEL_STREAM, MNB_KERNEL_GEMV_GROUP, MNB_KERNEL_GEMM = 1, 2, 3, 4
+MNB_KERNEL_GEMV, MNB_KERNEL_STREAM, MNB_KERNEL_GEMV_GROUP, MNB_KERNEL_GEMM, MNB_KERNEL_KSLICE = 1, 2, 3, 4, 5
 MNB_ORDER_NONE, MNB_ORDER_STREAM_K, MNB_ORDER_TILE_LIST = 0, 1, 2
 
 
