@@ -671,7 +671,7 @@ def main():
                          "roofline": {"bound": "mfma", "achieved": round(kernel_tflops512s, 2),
                                       "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                       "frac": round(kernel_tflops512s / FP16_PEAK_TFLOPS, 4),
-                                      "kernel": "mnb::gemm_sk_kernel (M=512, one launch per projection)",
+                                      "kernel": "mnb::gemm_sk_kernel, mnb::gemm_ks_kernel for o_proj (M=512, one launch per projection)",
                                       "avg_launch_us": round(gpu512s / len(projs) * 1e6, 2),
                                       "traffic": measured_traffic("gemm_sk_phi3_prefill_m512.md",
                                                                   "traffic_bytes_per_step"),

@@ -21,10 +21,11 @@
 // row pieces), goes through a 4 KiB wave-private LDS block into operand order,
 // and feeds 4 x NTW v_mfma_f32_16x16x32_f16 (weights as A, x as B, so a
 // lane's four results are four consecutive columns of one row).  The next x
-// block is in flight while the current one is multiplied, and the weights of
-// the next one to three super-tiles (as many as the registers hold beside the
-// accumulators) while the current one's row blocks run.  All loads are ordinary loads, so the compiler places every
-// wait.
+// block is in flight while the current one is multiplied, and the next
+// super-tile's weights while the current one's row blocks run.  All loads are
+// ordinary loads, so the compiler places every wait.  (Two x blocks, or two
+// and three super-tiles of weights, in flight measured no faster: at these
+// sizes a workgroup is bound by its CU's dequantization and MFMA issue.)
 #include <algorithm>
 
 #include "mnb_device.h"
@@ -285,9 +286,9 @@ int ks_waves(int ST) { return ST < kKsMaxWaves ? ST : kKsMaxWaves; }
 // projections (K 3072 and 8192, N 3072 to 32064, M 17 to 512): a workgroup
 // alone on its CU takes c + k us per super-tile of each wave; with more
 // workgroups than CUs the chip sustains thr wave-super-tiles per us (at 256
-// CUs).  The launch takes the longer of the two.  (4 x 1, 4 x 2 and 8 x 2
-// blocks were measured too; the model never prefers them, over 2100 shapes
-// from K 256 to 14336 and N 64 to 151936.)
+// CUs).  The launch takes the longer of the two.  (Output blocks of 64 x 16,
+// 64 x 32 and 128 x 32 were measured too; with their fitted costs the model
+// never prefers them over 2100 shapes from K 256 to 14336 and N 64 to 151936.)
 struct KsCost {
     int mb, ntw;
     double c, k, thr;
