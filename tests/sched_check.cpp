@@ -45,8 +45,9 @@ static int check_stream() {
     long total = 0, cost = 0, maxunit = 0;
     for (size_t i = 0; i < NT.size(); ++i) {
         total += NT[i];
-        cost += (long)NT[i] * (ST[i] + 1);
-        maxunit = std::max<long>(maxunit, ST[i] + 1);
+        const long job_tiles = 4L * ((ST[i] + 3) / 4);   // 4-tile jobs, the last one padded
+        cost += (long)NT[i] * (job_tiles + 1);
+        maxunit = std::max<long>(maxunit, job_tiles + 1);
     }
     if ((long)units.size() != total) return fail("unit count", (long)units.size(), total);
     if ((long)wb.size() != 2 * waves + 1) return fail("wave table size", (long)wb.size(), 2 * waves + 1);
@@ -64,10 +65,10 @@ static int check_stream() {
             if (it >= NT.size() || (long)t >= NT[it]) return fail("unit code", (long)it, (long)t);
             if (seen[it][t]++) return fail("unit twice", (long)it, (long)t);
             if (k > b && units[(size_t)k - 1] >= u) return fail("wave order", w, k);
-            jobs += ST[it];
-            c += ST[it] + 1;
+            jobs += (ST[it] + 3) / 4;
+            c += 4L * ((ST[it] + 3) / 4) + 1;
         }
-        if (jobs != wb[(size_t)(2 * w + 1)]) return fail("wave super-tiles", w, jobs);
+        if (jobs != wb[(size_t)(2 * w + 1)]) return fail("wave jobs", w, jobs);
         maxcost = std::max(maxcost, c);
         busy += e > b;
     }

@@ -82,7 +82,8 @@ bool stream_schedule(const std::vector<int32_t> &NT, const std::vector<int32_t> 
     std::vector<std::pair<int32_t, uint32_t>> order;   // (cost, code)
     for (size_t i = 0; i < NT.size(); ++i) {
         if (NT[i] < 1 || NT[i] > 65536 || ST[i] < 1) return false;
-        for (int32_t nt = 0; nt < NT[i]; ++nt) order.emplace_back(ST[i] + 1, ((uint32_t)i << 16) | (uint32_t)nt);
+        const int32_t cost = kStreamJobTiles * stream_jobs(ST[i]) + 1;
+        for (int32_t nt = 0; nt < NT[i]; ++nt) order.emplace_back(cost, ((uint32_t)i << 16) | (uint32_t)nt);
     }
     std::stable_sort(order.begin(), order.end(),
                      [](const std::pair<int32_t, uint32_t> &a, const std::pair<int32_t, uint32_t> &b) {
@@ -104,7 +105,7 @@ bool stream_schedule(const std::vector<int32_t> &NT, const std::vector<int32_t> 
     for (auto &v : per) {
         std::sort(v.begin(), v.end());
         int64_t jobs = 0;
-        for (uint32_t c : v) jobs += ST[c >> 16];
+        for (uint32_t c : v) jobs += stream_jobs(ST[c >> 16]);
         if (jobs > std::numeric_limits<int32_t>::max()) return false;
         wave_begin.push_back((int32_t)units.size());
         wave_begin.push_back((int32_t)jobs);

@@ -104,16 +104,23 @@ MNB_HD inline int32_t sk_cf_tile(int32_t MT, int32_t NG, int32_t q) {
     return m0 + within / nn + (n0 + within % nn) * MT;
 }
 
+// The streaming kernel's unit of issue: up to kStreamJobTiles consecutive
+// super-tiles of one n-tile (a unit of ST super-tiles is stream_jobs(ST)
+// jobs; the last job of a unit whose ST is not a multiple re-reads its last
+// super-tile for the missing ones, against zero activations).
+constexpr int32_t kStreamJobTiles = 4;
+MNB_HD inline int32_t stream_jobs(int32_t ST) { return (ST + kStreamJobTiles - 1) / kStreamJobTiles; }
+
 // Static schedule of a group of M = 1 products on the persistent streaming
 // kernel (mnb_stream.hip).  A unit is one 16-row n-tile of one item over its
 // whole K, coded (item << 16) | n-tile; item i has NT[i] n-tiles of ST[i]
-// super-tiles.  Units are dealt longest first (cost = super-tiles + 1, the
-// unit's output write counted as one) to the least loaded of `waves` waves;
-// each wave keeps its units in group order.  Fills units (wave-major) and
-// wave_begin (2 * waves + 1 entries: per wave its first unit and the number of
-// super-tiles of its units, then the end of the list).  Returns false when
-// there are 65536 items or more, an item has more than 65536 n-tiles, or a
-// wave's super-tiles do not fit 31 bits.
+// super-tiles.  Units are dealt longest first (cost = the super-tiles its
+// jobs read + 1, the unit's output write counted as one) to the least loaded
+// of `waves` waves; each wave keeps its units in group order.  Fills units
+// (wave-major) and wave_begin (2 * waves + 1 entries: per wave its first unit
+// and the number of jobs of its units, then the end of the list).  Returns
+// false when there are 65536 items or more, an item has more than 65536
+// n-tiles, or a wave's jobs do not fit 31 bits.
 bool stream_schedule(const std::vector<int32_t> &NT, const std::vector<int32_t> &ST, int64_t waves,
                      std::vector<uint32_t> &units, std::vector<int32_t> &wave_begin);
 

@@ -3,11 +3,18 @@
 // A recorded group (mnb_group_create) of independent decode projections is
 // cut into units: one unit = one 16-row n-tile of one item, over its whole K.
 // Each wavefront owns a list of units (balanced by bytes on the host, see
-// mnb_api.cpp) and streams their 16x128 weight tiles through a 4-deep
-// register pipeline that runs across unit boundaries, so every wave keeps
-// four 1 KiB tile loads in flight at all times.  A wave finishes a unit on
-// its own (no split-K, no cross-wave reduction, no barrier) and writes the
-// unit's 16 outputs.  The grid is sized to the device's resident capacity;
+// mnb_sched.cpp) and streams them as jobs of kStreamJobTiles (4) consecutive
+// super-tiles through a 2-deep register pipeline that runs across unit
+// boundaries, so every wave keeps 8 KiB of tile loads in flight at all times.
+// A job's loads are four 1 KiB weight tiles (one 16-byte non-temporal load per
+// lane each), ONE scale load and ONE zero-point load for all four tiles (lane
+// group g brings tile g's row), and ONE 1 KiB load of the four tiles'
+// activations: per tile, a third of the load instructions of a per-tile
+// pipeline (the scale and activation loads, not their bytes, cost 13% of the
+// launch).  The scales, zero points and activations go through a
+// wave-private LDS block to the lanes that multiply them.  A wave finishes a
+// unit on its own (no split-K, no cross-wave reduction, no barrier) and writes
+// the unit's 16 outputs.  The grid is sized to the device's resident capacity;
 // the kernel is a plain loop over a static list, so no wave ever waits for
 // another.
 #include "mnb_device.h"
@@ -15,20 +22,24 @@
 namespace mnb {
 
 #ifndef MNB_STREAM_DEPTH
-#define MNB_STREAM_DEPTH 4
+#define MNB_STREAM_DEPTH 2
 #endif
-constexpr int kStreamDepth = MNB_STREAM_DEPTH;   // tiles in flight per wave
+constexpr int kStreamDepth = MNB_STREAM_DEPTH;   // jobs in flight per wave
 constexpr int kStreamWaves = 4;      // waves per workgroup
+constexpr int kJT = kStreamJobTiles;
+
+typedef uint32_t u32x4_st_alias_t __attribute__((ext_vector_type(4), may_alias));
+typedef _Float16 half8_st_alias_t __attribute__((ext_vector_type(8), may_alias));
 
 // Per-unit view of one item, resolved with uniform (scalar) loads.
 template <typename ScaleT>
 struct UnitRef {
     const u32x4_t *q;      // first tile of the n-tile, + lane
-    const ScaleT *s;       // first scale row of the n-tile
-    const uint8_t *z;      // first zero-point row of the n-tile
+    const ScaleT *s;       // first scale row of the n-tile, + row r
+    const uint8_t *z;      // first zero-point row of the n-tile, + row r
     const _Float16 *x;     // activation row
     void *y;
-    int32_t ST, kx, N, nt, y_f16, accumulate;
+    int32_t ST, NJ, kx, N, nt, y_f16, accumulate;
     float unfold;
 };
 
@@ -46,6 +57,7 @@ __device__ __forceinline__ UnitRef<ScaleT> resolve_unit(const GroupItem *__restr
     u.x = p.x;
     u.y = p.y;
     u.ST = p.ST;
+    u.NJ = stream_jobs(p.ST);
     u.kx = p.kx;
     u.N = p.N;
     u.nt = nt;
@@ -60,85 +72,110 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
                                                                         const uint32_t *__restrict__ units,
                                                                         const int32_t *__restrict__ wave_begin) {
     constexpr int ZB = SPS <= 2 ? 1 : SPS / 2;
+    constexpr int SB = SPS * (int)sizeof(ScaleT);               // scale bytes per row per tile
     constexpr int D = kStreamDepth;
-    __shared__ __align__(16) _Float16 xs_all[kStreamWaves][D][kTileK];
+    // per wave: a job's activations (4 x 128 fp16), scale rows and zero-point
+    // entries (4 tiles x 16 rows each)
+    constexpr int kXB = kJT * kTileK * 2, kSB = kJT * kTileRows * SB, kZB = HAS_ZP ? kJT * kTileRows * ZB : 0;
+    constexpr int kWaveLds = kXB + kSB + kZB;
+    __shared__ __align__(16) unsigned char lds_all[kStreamWaves * kWaveLds];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, gg = lane >> 4;
     const int gw = blockIdx.x * kStreamWaves + wave;
     const int ubeg = wave_begin[2 * gw], uend = wave_begin[2 * gw + 2];
-    const int njobs = wave_begin[2 * gw + 1];   // super-tiles over all of this wave's units
+    const int njobs = wave_begin[2 * gw + 1];   // jobs over all of this wave's units
     if (ubeg >= uend) return;
     const uint32_t k6400 = vgpr_const(0x64006400u);
     const u32x4_t zero4 = {0u, 0u, 0u, 0u};
+    unsigned char *xw = lds_all + wave * kWaveLds;   // activations
+    unsigned char *sw = xw + kXB;                    // scale rows
+    unsigned char *zw = sw + kSB;                    // zero-point entries
 
-    u32x4_t raw[D];
-    ScaleT sv[D][SPS];
+    u32x4_t raw[D][kJT];
+    ScaleT sv[D][SPS];   // lane group g: tile g's scale row r
     uint32_t zb[D];
     u32x4_t xv[D];
-    bool xok[D];   // this lane's x piece lies below kx (applied at compute time, not at load time)
+    bool xok[D];         // this lane's activation piece lies below kx (applied when it is written to LDS)
 
-    // issue cursor: unit index iu, super-tile ist
-    int iu = ubeg, ist = 0;
+    // issue cursor: unit index iu, job ij
+    int iu = ubeg, ij = 0;
     UnitRef<ScaleT> iref = resolve_unit<ScaleT, SPS, ZB>(items, units[iu], lane, r);
     // Every call issues the same loads (past the last job it re-loads the last
-    // tile, which is never computed), so the loop below has a fixed number of
-    // loads in flight and exact wait counts.
+    // job, which is never computed; past a unit's last super-tile a job
+    // re-loads that super-tile, whose activations are zero), so the loop below
+    // has a fixed number of loads in flight and exact wait counts.
     auto issue = [&](int d) {
-        raw[d] = gld_nt(iref.q + (size_t)ist * 64);
-        load_scale_row<ScaleT, SPS>(iref.s + (size_t)ist * kTileRows * SPS, sv[d]);
-        if constexpr (HAS_ZP) zb[d] = load_zp<ZB>(iref.z + (size_t)ist * kTileRows * ZB);
+        const int st0 = ij * kJT;
+#pragma unroll
+        for (int t = 0; t < kJT; ++t) raw[d][t] = gld_nt(iref.q + (size_t)min(st0 + t, iref.ST - 1) * 64);
+        const int stg = min(st0 + gg, iref.ST - 1);
+        load_scale_row<ScaleT, SPS>(iref.s + (size_t)stg * kTileRows * SPS, sv[d]);
+        if constexpr (HAS_ZP) zb[d] = load_zp<ZB>(iref.z + (size_t)stg * kTileRows * ZB);
         else zb[d] = 0x88888888u;
-        // lanes 0..15 bring this tile's 128 activations
-        const int k = ist * kTileK + 8 * lane;
+        // lane l brings activations k = st0 * 128 + 8 l .. + 7 (tile l / 16)
+        const int k = st0 * kTileK + 8 * lane;
         xv[d] = gld((const u32x4_t *)(iref.x + min(k, iref.kx - 8)));
-        xok[d] = lane < kTileK / 8 && k < iref.kx;
-        if (ist + 1 < iref.ST) {
-            ++ist;
+        xok[d] = k < iref.kx;
+        if (ij + 1 < iref.NJ) {
+            ++ij;
         } else if (iu + 1 < uend) {
-            ist = 0;
+            ij = 0;
             iref = resolve_unit<ScaleT, SPS, ZB>(items, units[++iu], lane, r);
         }
     };
 
-    // compute cursor: unit index cu, super-tile cst
-    int cu = ubeg, cst = 0;   // compute cursor (unit, super-tile)
+    // compute cursor: unit index cu, job cj
+    int cu = ubeg, cj = 0;
     UnitRef<ScaleT> cref = iref;
     float acc = 0.f;
     auto compute = [&](int d) {
-        _Float16 *xs = xs_all[wave][d];
-        if (lane < kTileK / 8) ((u32x4_t *)xs)[lane] = xok[d] ? xv[d] : zero4;   // wave-private, in-order LDS
-        half8_t xa[4];
+        // wave-private LDS: a wave's LDS accesses complete in order, and the
+        // compiler barriers keep this job's writes after the previous job's
+        // reads and its reads after its writes
+        *(u32x4_st_alias_t *)(xw + lane * 16) = xok[d] ? xv[d] : zero4;
+        __builtin_memcpy(sw + (gg * kTileRows + r) * SB, &sv[d][0], SB);
+        if constexpr (HAS_ZP) __builtin_memcpy(zw + (gg * kTileRows + r) * ZB, &zb[d], ZB);
+        asm volatile("" ::: "memory");
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xa[j] = *(const half8_t *)(xs + 32 * j + 8 * gg);
-        if constexpr (SPS == 8) {
-            float4_t dd = {0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < kJT; ++t) {
+            half8_t xa[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int i = 2 * j + (gg >> 1);
-                const uint32_t z = HAS_ZP ? zp_nibble(zb[d], i) : 8u;
-                half8_t b = unpack_q_minus_zp(raw[d][j], bias_lo_pair(z), bias_hi_pair(z), k6400);
-                b = b * (_Float16)(float)sv[d][i];
-                dd = mfma16x16x32(xa[j], b, dd);
-            }
-            acc += dd[0];
-        } else {
-            constexpr int KPB = 4 / SPS;
-#pragma unroll
-            for (int i = 0; i < SPS; ++i) {
-                const uint32_t z = HAS_ZP ? zp_nibble(zb[d], i) : 8u;
-                const uint32_t blo = bias_lo_pair(z), bhi = bias_hi_pair(z);
+            for (int j = 0; j < 4; ++j) xa[j] = *(const half8_st_alias_t *)(xw + t * (kTileK * 2) + (32 * j + 8 * gg) * 2);
+            ScaleT sc[SPS];
+            __builtin_memcpy(&sc[0], sw + (t * kTileRows + r) * SB, SB);
+            uint32_t zt = 0x88888888u;
+            if constexpr (HAS_ZP) __builtin_memcpy(&zt, zw + (t * kTileRows + r) * ZB, ZB);
+            if constexpr (SPS == 8) {
                 float4_t dd = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int u = 0; u < KPB; ++u) {
-                    const int j = i * KPB + u;
-                    dd = mfma16x16x32(xa[j], unpack_q_minus_zp(raw[d][j], blo, bhi, k6400), dd);
+                for (int j = 0; j < 4; ++j) {
+                    const int i = 2 * j + (gg >> 1);
+                    const uint32_t z = HAS_ZP ? zp_nibble(zt, i) : 8u;
+                    half8_t b = unpack_q_minus_zp(raw[d][t][j], bias_lo_pair(z), bias_hi_pair(z), k6400);
+                    b = b * (_Float16)(float)((gg >> 1) ? sc[2 * j + 1] : sc[2 * j]);
+                    dd = mfma16x16x32(xa[j], b, dd);
                 }
-                acc = fmaf((float)sv[d][i], dd[0], acc);
+                acc += dd[0];
+            } else {
+                constexpr int KPB = 4 / SPS;
+#pragma unroll
+                for (int i = 0; i < SPS; ++i) {
+                    const uint32_t z = HAS_ZP ? zp_nibble(zt, i) : 8u;
+                    const uint32_t blo = bias_lo_pair(z), bhi = bias_hi_pair(z);
+                    float4_t dd = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int u = 0; u < KPB; ++u) {
+                        const int j = i * KPB + u;
+                        dd = mfma16x16x32(xa[j], unpack_q_minus_zp(raw[d][t][j], blo, bhi, k6400), dd);
+                    }
+                    acc = fmaf((float)sc[i], dd[0], acc);
+                }
             }
         }
-        if (++cst == cref.ST) {
+        asm volatile("" ::: "memory");
+        if (++cj == cref.NJ) {
             // x was broadcast to all 16 MFMA rows: lanes 0..15 hold row 0, column r
             const int n = cref.nt * kTileRows + r;
             if (gg == 0 && n < cref.N) {
@@ -147,7 +184,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
                 else store_y<false>(cref.y, (size_t)n, v, cref.accumulate != 0);
             }
             acc = 0.f;
-            cst = 0;
+            cj = 0;
             if (cu + 1 < uend) cref = resolve_unit<ScaleT, SPS, ZB>(items, units[++cu], lane, r);
         }
     };
