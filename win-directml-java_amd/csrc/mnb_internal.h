@@ -201,7 +201,7 @@ struct GemvGroupPlan {
     int32_t max_m = 0;         // largest M of the items (M > 1: x row groups to load)
     // M == 1: persistent streaming schedule
     void *units = nullptr;       // device uint32_t[U]: (item << 16) | n-tile, grouped by wave
-    void *wave_begin = nullptr;  // device int32_t[2 * waves + 1]: per wave its first unit and super-tile count, then the end
+    void *wave_begin = nullptr;  // device int32_t[2 * waves + 1]: per wave its first unit and 4-super-tile job count, then the end
     int32_t stream_wgs = 0;
 };
 hipError_t launch_gemv_group(const GemvGroupPlan &g, hipStream_t stream);
