@@ -106,8 +106,8 @@ MNB_HD inline int32_t sk_cf_tile(int32_t MT, int32_t NG, int32_t q) {
 
 // The streaming kernel's unit of issue: up to kStreamJobTiles consecutive
 // super-tiles of one n-tile (a unit of ST super-tiles is stream_jobs(ST)
-// jobs; the last job of a unit whose ST is not a multiple re-reads its last
-// super-tile for the missing ones, against zero activations).
+// jobs; the last job of a unit whose ST is not a multiple loads its last
+// super-tile again for the missing ones and does not compute them).
 constexpr int32_t kStreamJobTiles = 4;
 MNB_HD inline int32_t stream_jobs(int32_t ST) { return (ST + kStreamJobTiles - 1) / kStreamJobTiles; }
 

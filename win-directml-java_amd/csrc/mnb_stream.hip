@@ -104,7 +104,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
     UnitRef<ScaleT> iref = resolve_unit<ScaleT, SPS, ZB>(items, units[iu], lane, r);
     // Every call issues the same loads (past the last job it re-loads the last
     // job, which is never computed; past a unit's last super-tile a job
-    // re-loads that super-tile, whose activations are zero), so the loop below
+    // re-loads that super-tile, which compute() skips), so the loop below
     // has a fixed number of loads in flight and exact wait counts.
     auto issue = [&](int d) {
         const int st0 = ij * kJT;
@@ -140,6 +140,9 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
         asm volatile("" ::: "memory");
 #pragma unroll
         for (int t = 0; t < kJT; ++t) {
+            // past the unit's last super-tile (K not a multiple of 512): loaded
+            // again for a fixed load count, not computed (a uniform branch)
+            if (cj * kJT + t >= cref.ST) break;
             half8_t xa[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) xa[j] = *(const half8_st_alias_t *)(xw + t * (kTileK * 2) + (32 * j + 8 * gg) * 2);
