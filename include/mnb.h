@@ -274,14 +274,14 @@ int32_t mnb_group_destroy(mnb_group *group);
 #define MNB_KERNEL_STREAM 2      /* persistent weight stream over (product, n-tile) units (M == 1 groups) */
 #define MNB_KERNEL_GEMV_GROUP 3  /* the GEMV kernel over every product's n-tiles (1 < M <= 16 groups) */
 #define MNB_KERNEL_GEMM 4        /* the MFMA GEMM */
-#define MNB_KERNEL_KSLICE 5      /* one product, M > 16: workgroup per output block, its waves split K (no split tiles) */
+#define MNB_KERNEL_KSLICE 5      /* one product, M >= 9: workgroup per output block, its waves split K (no split tiles) */
 #define MNB_ORDER_NONE 0         /* one unit of work per workgroup or a static unit list */
 #define MNB_ORDER_STREAM_K 1     /* (tile, k-stage) iterations cut into equal ranges; split tiles reduced after */
 #define MNB_ORDER_TILE_LIST 2    /* whole tiles per workgroup from a tile list (a table, or closed form for one product) */
 typedef struct mnb_plan_info {
     int32_t kernel;      /* MNB_KERNEL_* */
     int32_t order;       /* MNB_ORDER_* */
-    int32_t tile_rows;   /* output tile: rows of x (GEMM 32, 64 or 128; K-sliced 32, 64 or 128); 0 otherwise */
+    int32_t tile_rows;   /* output tile: rows of x (GEMM 32, 64 or 128; K-sliced 16 (M <= 16), 32, 64 or 128); 0 otherwise */
     int32_t tile_cols;   /* output tile: columns (GEMM 256 or 512; K-sliced 16, 32 or 64); 16 for the GEMV kernels */
     int32_t workgroups;  /* grid size */
 } mnb_plan_info;

@@ -35,18 +35,22 @@ def test_graph_capture_replays_match_eager():
         w_gu = _weight(ctx, 2, 16384, 3072)                # decode gate_up
         w_pf = _weight(ctx, 3, 9001, 8192, zp=True)        # prefill product with split tiles
         w_ks = _weight(ctx, 4, 1000, 3072, zp=True)        # prefill product on the K-sliced kernel
+        w_k16 = _weight(ctx, 5, 16384, 3072)               # M = 12 product on 16 x 64 K-sliced blocks
         assert w_pf.plan(200).as_tuple() == (mnb_hip.MNB_KERNEL_GEMM, mnb_hip.MNB_ORDER_STREAM_K, 128, 256)
         assert w_ks.plan(200).kernel == mnb_hip.MNB_KERNEL_KSLICE
+        assert w_k16.plan(12).as_tuple() == (mnb_hip.MNB_KERNEL_KSLICE, mnb_hip.MNB_ORDER_NONE, 16, 64)
         w_g = [_weight(ctx, 10 + i, 1536, 576, 64, zp=True) for i in range(3)]
         gen = torch.Generator(device=dev).manual_seed(7)
         x1 = torch.empty(3072, device=dev, dtype=torch.float16)
         xp = torch.empty(200, 8192, device=dev, dtype=torch.float16)
         xk = torch.empty(200, 3072, device=dev, dtype=torch.float16)
+        x12 = torch.empty(12, 3072, device=dev, dtype=torch.float16)
         xg = [torch.empty(576, device=dev, dtype=torch.float16) for _ in w_g]
         y_o = torch.empty(3072, device=dev, dtype=torch.float16)
         y_gu = torch.empty(16384, device=dev, dtype=torch.float32)
         y_pf = torch.empty(200, 9001, device=dev, dtype=torch.float16)
         y_ks = torch.empty(200, 1000, device=dev, dtype=torch.float32)
+        y_k16 = torch.empty(12, 16384, device=dev, dtype=torch.float16)
         y_g = [torch.empty(1536, device=dev, dtype=torch.float16) for _ in w_g]
         st = torch.cuda.Stream()
 
@@ -54,6 +58,7 @@ def test_graph_capture_replays_match_eager():
             x1.copy_(torch.randn(3072, device=dev, generator=gen).half())
             xp.copy_(torch.randn(200, 8192, device=dev, generator=gen).half())
             xk.copy_(torch.randn(200, 3072, device=dev, generator=gen).half())
+            x12.copy_(torch.randn(12, 3072, device=dev, generator=gen).half())
             for x in xg:
                 x.copy_(torch.randn(576, device=dev, generator=gen).half())
 
@@ -67,6 +72,7 @@ def test_graph_capture_replays_match_eager():
             w_gu.matmul(x1, y_gu, stream=st.cuda_stream)
             w_pf.matmul(xp, y_pf, stream=st.cuda_stream)
             w_ks.matmul(xk, y_ks, stream=st.cuda_stream)
+            w_k16.matmul(x12, y_k16, stream=st.cuda_stream)
             group.run(st.cuda_stream)
 
         graph = torch.cuda.CUDAGraph()
@@ -74,7 +80,7 @@ def test_graph_capture_replays_match_eager():
             record()
         torch.cuda.synchronize()
 
-        outs = [y_o, y_gu, y_pf, y_ks] + y_g
+        outs = [y_o, y_gu, y_pf, y_ks, y_k16] + y_g
         for rep in range(4):
             with torch.cuda.stream(st):
                 fill()
@@ -93,7 +99,7 @@ def test_graph_capture_replays_match_eager():
                 assert torch.equal(a.view(torch.int16) if a.dtype == torch.float16 else a.view(torch.int32),
                                    b.view(torch.int16) if b.dtype == torch.float16 else b.view(torch.int32)), (rep, i)
         group.close()
-        for w in [w_o, w_gu, w_pf, w_ks] + w_g:
+        for w in [w_o, w_gu, w_pf, w_ks, w_k16] + w_g:
             w.close()
         del graph
     finally:

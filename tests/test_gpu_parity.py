@@ -205,13 +205,28 @@ def test_config2_phi3_prefill_sampled_rows(ctx, M):
 # ------------------------------------------------ bitwise properties ------
 
 def test_rows_are_independent_in_skinny_kernel(ctx):
+    """On the GEMV a row's result does not depend on M (rows of an M = 16
+    product equal M = 1 products bit for bit).  A wide product at M = 16 runs
+    on 16 x 64 K-sliced blocks instead, whose K slices are summed in another
+    order: its rows match the M = 1 products to the tolerance, and repeated
+    calls are bitwise identical."""
     t = synth.make_weight(11, 3072, 3072, 32)
     w = upload(ctx, t)
+    assert w.plan(16).kernel == mnb_hip.MNB_KERNEL_GEMV, w.plan(16).as_tuple()
     x16 = synth.make_x(12, 16, 3072)
     y16 = w.matmul(x16)
     for m in (0, 5, 15):
         y1 = w.matmul(x16[m])
         assert np.array_equal(y1.view(np.uint32), y16[m].view(np.uint32)), m
+    w.close()
+    t = synth.make_weight(16, 9216, 3072, 32)
+    w = upload(ctx, t)
+    assert w.plan(16).as_tuple() == (KSLICE, NO_ORDER, 16, 64), w.plan(16).as_tuple()
+    y16 = w.matmul(x16)
+    assert np.array_equal(w.matmul(x16).view(np.uint32), y16.view(np.uint32))
+    tol = orc.tolerance(3072, x16.astype(np.float32), w.dequantize(np.float32))
+    for m in (0, 5, 15):
+        assert np.abs(w.matmul(x16[m]) - y16[m]).max() <= tol, m
     w.close()
 
 
@@ -311,14 +326,21 @@ def test_gemm_split_tiles_tails_and_outputs(ctx, M, K, N):
     (300, 4096, 1001, 128, True, False, (32, 64)),
     (130, 8192, 3072, 32, False, False, (32, 64)),
     (64, 3072, 9216, 32, False, False, (64, 64)),
-    (250, 3072, 3070, 32, True, False, (64, 64))],
+    (250, 3072, 3070, 32, True, False, (64, 64)),
+    # 9 <= M <= 16 with wide N: 16 x 64 blocks instead of the GEMV
+    (16, 3072, 16384, 32, False, False, (16, 64)),
+    (13, 2500, 16000, 64, True, False, (16, 64)),
+    (14, 1500, 30000, 16, False, False, (16, 64)),
+    (9, 3001, 20000, 128, True, False, (16, 64)),
+    (11, 3000, 16001, 32, False, True, (16, 64))],
     ids=lambda c: "M%d-K%d-N%d-bs%d%s%s" % (c[0], c[1], c[2], c[3], "-zp" if c[4] else "", "-f32s" if c[5] else ""))
 def test_single_products_k_sliced(ctx, case):
     """Single products where the GEMM would have few tiles run on the
     K-sliced kernel (workgroup = 16 MB rows x 16 NTW columns over the whole K,
     its waves' K slices summed in LDS in wave order): each of its four output
-    blocks, M, N and K tails (rows past M, n-tiles past N, a partial last
-    super-tile), zero points, bs 16 to 128, fp32 scales, fp16 and fp32
+    blocks (and the 16-row block that replaces the GEMV for 9 <= M <= 16 with
+    wide N), M, N and K tails (rows past M, n-tiles past N, a partial last
+    super-tile, K % 8 != 0), zero points, bs 16 to 128, fp32 scales, fp16 and fp32
     outputs, y +=, a y not aligned for 4-column stores.  Within the tolerance
     of the oracle, bitwise repeatable, fp16 output = fp32 output rounded, and
     y += equal to y0 + y."""
@@ -853,14 +875,19 @@ def test_single_products_in_closed_form_tile_order(ctx, case):
 
 
 def test_matmul_plan_reports_the_single_product_schedule(ctx):
-    """mnb_matmul_plan: the GEMV kernel up to M = 16; the K-sliced kernel
-    where the GEMM would have few tiles for the chip (o_proj and down at M
-    32 to 512, qkv at 32 and 64: 32 x 16 up to 64 x 64 output blocks);
+    """mnb_matmul_plan: the GEMV kernel up to M = 8, and up to 16 for
+    narrow products (o_proj); 16 x 64 K-sliced blocks for wide products at
+    M = 12 and 16 (qkv, gate_up); the K-sliced kernel where the GEMM would
+    have few tiles for the chip (o_proj and down at M 32 to 512, qkv at 32
+    and 64: 32 x 16 up to 64 x 64 output blocks);
     stream-K 128 x 256 tiles for the qkv shape at M = 512; closed-form
     128 x 512 tile lists for products with many tiles (the Phi-3 lm_head at
     M = 512 and gate_up at 2048)."""
     for (K, N, M), expect in [((3072, 9216, 1), (mnb_hip.MNB_KERNEL_GEMV, NO_ORDER, 0, 16)),
-                              ((3072, 9216, 16), (mnb_hip.MNB_KERNEL_GEMV, NO_ORDER, 0, 16)),
+                              ((3072, 9216, 8), (mnb_hip.MNB_KERNEL_GEMV, NO_ORDER, 0, 16)),
+                              ((3072, 3072, 16), (mnb_hip.MNB_KERNEL_GEMV, NO_ORDER, 0, 16)),
+                              ((3072, 9216, 16), (KSLICE, NO_ORDER, 16, 64)),
+                              ((3072, 16384, 12), (KSLICE, NO_ORDER, 16, 64)),
                               ((3072, 3072, 32), (KSLICE, NO_ORDER, 32, 16)),
                               ((3072, 3072, 64), (KSLICE, NO_ORDER, 32, 32)),
                               ((3072, 9216, 32), (KSLICE, NO_ORDER, 32, 64)),

@@ -55,9 +55,10 @@ def _both(ctx, w, x, ydt, acc=False):
 
 
 # (M, K, N, zero points, x dtype, unaligned x, y dtype, y +=): split GEMM
-# tiles (stream-K partials in the scratch array), the K-sliced kernel, staged
-# x (fp32, K % 8 != 0, a misaligned pointer), the M <= 16 kernels; each case
-# is followed by a smaller one of the same kind.
+# tiles (stream-K partials in the scratch array), the K-sliced kernel (also
+# with 16-row blocks at M <= 16), staged x (fp32, K % 8 != 0, a misaligned
+# pointer), the M <= 16 kernels; each case is followed by a smaller one of
+# the same kind.
 CASES = [
     ((200, 8192, 9001, False, "f16", False, "f16", False), (150, 8192, 9001, False, "f16", False, "f16", False)),
     ((200, 3072, 1000, False, "f16", False, "f16", False), (130, 3072, 1000, False, "f16", False, "f16", False)),
@@ -66,6 +67,7 @@ CASES = [
     ((129, 3072, 3072, False, "f16", True, "f16", False), (17, 3072, 3072, False, "f16", True, "f16", False)),
     ((1, 3072, 9216, False, "f32", False, "f16", False), (1, 3072, 3072, False, "f16", False, "f32", True)),
     ((16, 1003, 500, True, "f32", False, "f16", False), (5, 1003, 500, True, "f16", True, "f16", False)),
+    ((16, 3001, 16000, True, "f32", False, "f16", False), (12, 3001, 16000, True, "f16", True, "f32", True)),
 ]
 
 
@@ -89,6 +91,8 @@ def test_noalloc_equals_matmul_twice(ctx, pair):
             ydt_t = torch.float16 if ydt == "f16" else torch.float32
             if (M, K, N) in ((200, 8192, 9001), (150, 8192, 9001)):
                 assert w.plan(M).as_tuple() == (mnb_hip.MNB_KERNEL_GEMM, mnb_hip.MNB_ORDER_STREAM_K, 128, 256), label
+            if (K, N) == (3001, 16000):
+                assert w.plan(M).as_tuple() == (mnb_hip.MNB_KERNEL_KSLICE, mnb_hip.MNB_ORDER_NONE, 16, 64), label
             ya, yb = _both(ctx, w, xt, ydt_t, acc)
             assert torch.equal(ya.view(torch.int16 if ydt == "f16" else torch.int32),
                                yb.view(torch.int16 if ydt == "f16" else torch.int32)), label

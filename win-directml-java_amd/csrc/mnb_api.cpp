@@ -587,6 +587,15 @@ int32_t mnb_matmul_plan(const mnb_context *ctx, const mnb_weight *w, int32_t M, 
     *out = mnb_plan_info{};
     const WeightGeom &g = w->g;
     if (M <= mnb::kSkinnyMaxM) {
+        const mnb::KsPlan kp = mnb::ks_skinny_plan(g, M, ctx->cu_count);
+        if (kp.wgs > 0) {
+            out->kernel = MNB_KERNEL_KSLICE;
+            out->order = MNB_ORDER_NONE;
+            out->tile_rows = 16 * kp.c.mb;
+            out->tile_cols = 16 * kp.c.ntw;
+            out->workgroups = (int32_t)kp.wgs;
+            return ok();
+        }
         out->kernel = MNB_KERNEL_GEMV;
         out->tile_cols = mnb::kTileRows;
         out->workgroups = g.NT;
@@ -698,7 +707,11 @@ hipError_t mnb::launch_product(const mnb_weight *w, int cu_count, int32_t M, con
     a.y = y;
     a.y_type = y_type;
     a.accumulate = accumulate ? 1 : 0;
-    return M <= mnb::kSkinnyMaxM ? mnb::launch_gemv(w, a, cu_count, s) : launch_prefill(w, cu_count, a, (float *)sk_ws, s);
+    if (M > mnb::kSkinnyMaxM) return launch_prefill(w, cu_count, a, (float *)sk_ws, s);
+    // M <= 16: the K-sliced kernel where its cost model expects a clear gain
+    // over the GEMV (9 <= M <= 16 and wide N)
+    const mnb::KsPlan kp = mnb::ks_skinny_plan(g, M, cu_count);
+    return kp.wgs > 0 ? mnb::launch_gemm_ks(w, a, kp.c, s) : mnb::launch_gemv(w, a, cu_count, s);
 }
 
 extern "C" {

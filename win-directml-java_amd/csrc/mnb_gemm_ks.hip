@@ -3,7 +3,9 @@
 //
 // Replaces, for single products, the batched shader INT4_MATMUL_BATCH_TILED_HLSL
 // (directml-windows-bindings/src/main/java/com/aresstack/windirectml/windows/
-// MatMulNBitsKernel.java:732-820) where the stream-K GEMM has too few tiles:
+// MatMulNBitsKernel.java:732-820) where the stream-K GEMM has too few tiles,
+// and for 9 <= M <= 16 the matvec shader's role (INT4_MATVEC_HLSL, :235-292)
+// where its cost model beats the GEMV's:
 // y[m,n] = sum_blk scale[n,blk] * sum_k (q[n,k]-zp[n,blk]) * x[m,k].
 //
 // Work decomposition: workgroup (m-block, n-group) computes 16 MB rows of y by
@@ -18,9 +20,10 @@
 // ((q - zp) * scale, as the GEMM does) and uses them for all MB row blocks of
 // x.  Each 16-row x block (16 x 128 fp16) is loaded row-contiguous (lane l
 // brings 16 bytes of row 4 i + l / 16, so a load covers four whole 256-byte
-// row pieces), goes through a 4 KiB wave-private LDS block into operand order,
-// and feeds 4 x NTW v_mfma_f32_16x16x32_f16 (weights as A, x as B, so a
-// lane's four results are four consecutive columns of one row).  The next x
+// row pieces), goes through a 4 KiB wave-private LDS block into operand
+// order, and feeds 4 x NTW
+// v_mfma_f32_16x16x32_f16 (weights as A, x as B, so a lane's four results
+// are four consecutive columns of one row).  The next x
 // block is in flight while the current one is multiplied, and the next
 // super-tile's weights while the current one's row blocks run.  All loads are
 // ordinary loads, so the compiler places every wait.  (Two x blocks, or two
@@ -254,10 +257,12 @@ static hipError_t ks_shape(const KsConfig &c, dim3 grid, dim3 block, hipStream_t
         hipLaunchKernelGGL((gemm_ks_kernel<ScaleT, HAS_ZP, SPS, MB_, NTW_>), grid, block, 0, s, p);     \
         return hipGetLastError();                                                                       \
     }
+    MNB_KS(1, 4)
     MNB_KS(2, 1)
     MNB_KS(2, 2)
     MNB_KS(2, 4)
-    MNB_KS(4, 4)
+    // 16 output units per wave: compiled where ks_config_supported allows it
+    if constexpr (SPS != 8 && !(sizeof(ScaleT) == 4 && HAS_ZP)) MNB_KS(4, 4)
 #undef MNB_KS
     return hipErrorInvalidValue;
 }
@@ -275,6 +280,7 @@ static hipError_t ks_sps(int sps, const KsConfig &c, dim3 grid, dim3 block, hipS
 
 bool ks_config_supported(int mb, int ntw, int scale_f32, int has_zp, int sps) {
     if (mb == 2 && (ntw == 1 || ntw == 2 || ntw == 4)) return true;
+    if (mb == 1 && ntw == 4) return true;   // 9 <= M <= 16 (ks_skinny_plan)
     // 16 output units per wave leave registers for the weights of one
     // super-tile only where their scales and zero points are small
     return mb == 4 && ntw == 4 && sps != 8 && !(scale_f32 && has_zp);
@@ -315,6 +321,61 @@ KsPlan ks_single_plan(int M, int NT, int ST, int scale_f32, int has_zp, int sps,
         if (best.wgs == 0 || est < best.est) best = KsPlan{c, est, wgs};
     }
     return best;
+}
+
+// Products with 9 <= M <= 16: the GEMV (one workgroup per n-tile, so every
+// n-tile reads all 16 x rows again) or this kernel with 16 x 64 output blocks
+// (x read once per four n-tiles, each weight tile dequantized once).  Model
+// of either launch, fitted to timings on MI355X of 40 shapes (K 896 to
+// 14336, N 896 to 151936, the weights read from HBM) at M = 12 and 16 for the
+// GEMV (median error 4%) and M = 2 to 16 for this kernel (5%): c plus the
+// longest of a workgroup's chain of super-tiles per wave (per round of
+// workgroups), the weight bytes at the chip's rate, the weight bytes at the
+// rate of the CUs the grid occupies, and the L2 reads (1 KiB of weights and
+// 4 KiB of x per tile of an n-tile group), plus a cost per workgroup.  Sizes
+// in KiB, times in us.  With M <= 8 the GEMV loads only one or two groups of
+// four x rows; there it was faster than this kernel, or within the models'
+// error, on every shape timed, and it always runs.  (16 x 16 and 16 x 32
+// blocks were timed too: with their fitted costs the choice gained nothing.)
+struct SkinnyCost {
+    double c, lat, bw, bw_cu, bw_l2, per_wg;
+};
+static const SkinnyCost kSkinnyGemv = {2.6154, 0.3196, 2343.2, 11.564, 11678.7, 0.0};
+static const SkinnyCost kSkinnyKs = {2.6868, 1.3758, 4589.1, 22.452, 8273.8, 1.4969};
+constexpr int kSkinnyMinM = 9, kSkinnyNTW = 4;
+// This kernel runs only where its estimate is this fraction of the GEMV's or
+// less.  Over the shapes timed at M = 12 and 16: the GEMV alone 840 us in
+// total, this choice 738 (no shape slower than with the GEMV), the faster
+// kernel per shape 737.
+constexpr double kSkinnyMargin = 0.92;
+
+static double skinny_est(const SkinnyCost &k, int64_t wgs, int spw, double w_kib, double l2_kib, int cu) {
+    const double chain = (double)((wgs + cu - 1) / cu) * spw * k.lat;
+    const double occupied = (double)std::min<int64_t>(wgs, cu);
+    const double t = std::max(std::max(chain, w_kib / k.bw), std::max(w_kib / (k.bw_cu * occupied), l2_kib / k.bw_l2));
+    return k.c + t + k.per_wg * (double)wgs / cu;
+}
+
+KsPlan ks_skinny_plan(const WeightGeom &g, int32_t M, int32_t cu_count) {
+    KsPlan none{{0, 0}, 0.0, 0};
+    if (M < kSkinnyMinM || M > kSkinnyMaxM || g.ST < 1) return none;
+    // the launch limits of launch_gemm_ks (x rows padded to a multiple of 8)
+    if ((uint64_t)g.NT * (uint64_t)g.ST * kTileBytes >= ((uint64_t)1 << 32)) return none;
+    if ((int64_t)M * ((g.K + 7) & ~7) * 2 > ((int64_t)1 << 31)) return none;
+    const KsConfig c{1, kSkinnyNTW};
+    if (!ks_config_supported(c.mb, c.ntw, g.scale_f32, g.has_zp, g.SPS)) return none;
+    const int cu = cu_count > 0 ? cu_count : 256;
+    const int ST = g.ST;
+    const double w_kib = (double)g.NT * ST;
+    // the GEMV: waves of 2 super-tiles, at most kGemvMaxWavesRows of them, looping beyond
+    const int gw = std::min((ST + 1) / 2, kGemvMaxWavesRows);
+    const int gspw = std::min(ST > 2 * gw ? (ST + 2 * gw - 1) / (2 * gw) * 2 : 2, ST);
+    none.est = skinny_est(kSkinnyGemv, g.NT, gspw, w_kib, w_kib * 5.0, cu);
+    // this kernel: ks_waves(ST) waves on contiguous K slices
+    const int kw = ks_waves(ST);
+    const int64_t wgs = ks_workgroups(M, g.NT, c);
+    const double est = skinny_est(kSkinnyKs, wgs, (ST + kw - 1) / kw, w_kib, w_kib * (1.0 + 4.0 / c.ntw), cu);
+    return est <= kSkinnyMargin * none.est ? KsPlan{c, est, wgs} : none;
 }
 
 int64_t ks_workgroups(int M, int NT, const KsConfig &c) {

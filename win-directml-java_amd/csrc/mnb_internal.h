@@ -298,6 +298,10 @@ KsPlan ks_single_plan(int M, int NT, int ST, int scale_f32, int has_zp, int sps,
 // How one product (one chunk of at most 2 GiB of x rows, M > 16) runs: the
 // K-sliced kernel when its cost model expects it to finish before the GEMM's
 // plan, else that plan.
+// How one product with M <= 16 runs: for 9 <= M <= 16 the K-sliced kernel
+// with 16-row blocks where its cost model expects it to beat the GEMV's by a
+// margin, else the GEMV (wgs == 0).
+KsPlan ks_skinny_plan(const WeightGeom &g, int32_t M, int32_t cu_count);
 struct ProductPlan {
     bool ks;
     KsConfig kc;
