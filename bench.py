@@ -24,6 +24,9 @@ M=512, Phi-3-mini shapes"):
 * qwen: the Qwen2.5-0.5B tied lm_head (quantized on the device, M=1) and the
   Qwen step with a quantized lm_head (97 projections, bs 32) as one group
   launch at M=1 and M=64.
+* phi3_export_variant: the same 129 Phi-3 projections in the weight format
+  of the reference's DirectML int4 export (block size 128, explicit uint8
+  zero points, fp16 scales) as one group launch at M=1 and at M=512.
 * cpu_baseline: the oracle's restatement of the reference's Java CPU path
   (8-lane FMA block dot, one thread per core) on a bounded sample of the
   same decode step.
@@ -65,11 +68,11 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-sweep", action="store_true")
     p.add_argument("--eager", action="store_true", help="launch directly instead of via HIP graphs (counter runs)")
-    p.add_argument("--phase", choices=("all", "decode", "chain", "prefill", "qwen", "config0"), default="all",
+    p.add_argument("--phase", choices=("all", "decode", "chain", "prefill", "qwen", "config0", "export"), default="all",
                    help="decode: only the M=1 group launch and the copy calibration; chain: only the 129 M=1 "
                         "launches in stream order (a HIP graph); prefill: only the M=512 launches (both for "
                         "counter runs); qwen: only the Qwen2.5-0.5B step at M=1 and 64; config0: only the single "
-                        "qkv product at M=1")
+                        "qkv product at M=1; export: only the Phi-3 step in the export's weight format")
     p.add_argument("--prefill-group", action="store_true",
                    help="with --phase prefill: the 129 projections as one group launch instead of 129 launches")
     p.add_argument("--prefill-m", type=int, default=512, help="with --phase prefill: rows M of the prefill step")
@@ -202,6 +205,27 @@ def copy_bandwidth(torch, stream):
     t = e0.elapsed_time(e1) / 1e3 / 10
     del a, b
     return 2 * n / t / 1e9
+
+
+def torch_read_bandwidth(torch, stream):
+    """Read rate of torch's fastest whole-buffer reduction found here (an
+    int64 sum over 4 GiB): a reference point for reads, like the copy
+    figure, not a ceiling."""
+    n = 4 << 30
+    a = torch.ones(n // 8, dtype=torch.int64, device="cuda")
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            a.sum()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(10):
+            a.sum()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) / 1e3 / 10
+    del a
+    return n / t / 1e9
 
 
 def measured_traffic(kernel_profile, key="traffic_bytes_per_launch"):
@@ -352,6 +376,60 @@ def config0_qkv(torch, mnb_hip, ctx, stream, args):
             "timing": "GPU time of graph replays of 68 back-to-back launches over 17 weight copies (272 MB) / 68"}
 
 
+def phi3_export_variant(torch, mnb_hip, ctx, stream, args):
+    """The Phi-3-mini step in the weight format of the reference's DirectML
+    int4 export (model/phi3-mini-directml-int4/directml/
+    directml-int4-awq-block-128: block size 128, explicit uint8 zero points
+    in the ONNX row-padded layout, fp16 scales), seeded random weights: the
+    129 projections as one group launch at M=1 (GB/s of algorithmic bytes,
+    zero points included) and at M=512 (TFLOP/s)."""
+    from mnb_hip import synth
+    bs = 128
+    projs = synth.phi3_decode_step()
+    host, ws = [], []
+    for i, (_, _, K, N) in enumerate(projs):
+        t = synth.make_weight(30_000 + i, N, K, bs, with_zp=True)
+        host.append(t)
+        ws.append(mnb_hip.Weight(ctx, N, K, bs, t.q, t.scales_f16, t.zp_row_padded, mnb_hip.MNB_ZP_ROW_PADDED))
+    gen = torch.Generator(device="cuda").manual_seed(128)
+    out = {"projections": len(projs), "block_size": bs, "zero_points": "explicit, uint8 row-padded (ONNX layout)"}
+    for M in (1, 512):
+        if M == 1:
+            xs = [torch.randn(K, device="cuda", generator=gen).half() for (_, _, K, _) in projs]
+        else:
+            xk = {K: torch.randn(M, K, device="cuda", generator=gen).half() for (_, _, K, _) in projs}
+            xs = [xk[K] for (_, _, K, _) in projs]
+        ys = [torch.empty(M, N, device="cuda", dtype=torch.float16) for (_, _, _, N) in projs]
+        grp = mnb_hip.Group(ctx, list(zip(ws, xs, ys)))
+        with torch.cuda.stream(stream):
+            grp.run(stream.cuda_stream)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            grp.run(stream.cuda_stream)
+        wall, gpu = time_graph(torch, g, stream, args.steps, args.warmup, args.settle_ms)
+        del g
+        grp.close()
+        if M == 1:
+            nbytes = sum(t.algorithmic_bytes(1) for t in host)
+            e = {"us_per_step": round(wall * 1e6, 2), "gpu_us_per_step": round(gpu * 1e6, 2), "bytes_per_step": nbytes,
+                 "gbs": round(nbytes / wall / 1e9, 1), "frac_hbm_peak": round(nbytes / wall / 1e9 / HBM_PEAK_GBS, 4),
+                 "kernel": "mnb::gemv_stream_kernel (one launch per step)"}
+            log("export-format step M=1 as one group launch: %.1f us, %.1f GB/s" % (wall * 1e6, e["gbs"]))
+        else:
+            flops = sum(2.0 * M * N * K for (_, _, K, N) in projs)
+            e = {"us_per_step": round(wall * 1e6, 2), "gpu_us_per_step": round(gpu * 1e6, 2),
+                 "tflops": round(flops / wall / 1e12, 2), "frac_fp16_peak": round(flops / wall / 1e12 / FP16_PEAK_TFLOPS, 4),
+                 "kernel": "mnb::gemm_sk_kernel (one group launch per step)"}
+            log("export-format step M=512 as one group launch: %.1f us, %.1f TFLOP/s" % (wall * 1e6, e["tflops"]))
+        out["m%d" % M] = e
+        del xs, ys
+        torch.cuda.empty_cache()
+    for w in ws:
+        w.close()
+    return out
+
+
 def qwen_step(torch, mnb_hip, ctx, stream, args):
     """Qwen2.5-0.5B-shaped q4f16 step with a quantized lm_head: 24 layers x
     {qkv 896->1152, o 896->896, gate_up 896->9728, down 4864->896} + lm_head
@@ -420,6 +498,11 @@ def main():
     stream = torch.cuda.Stream()
     if args.phase == "qwen":
         print(json.dumps({"phase": "qwen", "qwen_step": qwen_step(torch, mnb_hip, ctx, stream, args)}), flush=True)
+        ctx.close()
+        return
+    if args.phase == "export":
+        print(json.dumps({"phase": "export", "phi3_export_variant": phi3_export_variant(torch, mnb_hip, ctx, stream, args)}),
+              flush=True)
         ctx.close()
         return
     if args.phase == "config0":
@@ -603,6 +686,8 @@ def main():
 
     copy_gbs = copy_bandwidth(torch, stream)
     log("device copy bandwidth: %.0f GB/s" % copy_gbs)
+    read_gbs = torch_read_bandwidth(torch, stream)
+    log("torch int64 sum read rate: %.0f GB/s" % read_gbs)
 
     for w in weights:
         w.close()
@@ -611,6 +696,8 @@ def main():
     cfg0 = config0_qkv(torch, mnb_hip, ctx, stream, args)
     qwen_head = qwen_tied_lm_head(torch, mnb_hip, ctx, stream, args)
     qwen = qwen_step(torch, mnb_hip, ctx, stream, args)
+    torch.cuda.empty_cache()
+    export = phi3_export_variant(torch, mnb_hip, ctx, stream, args)
     ctx.close()
 
     cpu = None
@@ -680,9 +767,11 @@ def main():
                                                         "(rocprofv3 FETCH_SIZE + WRITE_SIZE)"},
                          "sweep_tflops": sweep_seq},
         "device_copy_gbs": round(copy_gbs, 1),
+        "torch_read_gbs": round(read_gbs, 1),
         "config0_single_qkv": cfg0,
         "qwen_tied_lm_head": qwen_head,
         "qwen_step": qwen,
+        "phi3_export_variant": export,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
