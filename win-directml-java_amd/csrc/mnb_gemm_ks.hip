@@ -328,7 +328,10 @@ KsPlan ks_single_plan(int M, int NT, int ST, int scale_f32, int has_zp, int sps,
 // (x read once per four n-tiles, each weight tile dequantized once).  Model
 // of either launch, fitted to timings on MI355X of 40 shapes (K 896 to
 // 14336, N 896 to 151936, the weights read from HBM) at M = 12 and 16 for the
-// GEMV (median error 4%) and M = 2 to 16 for this kernel (5%): c plus the
+// GEMV (median error 4%) and M = 2 to 16 for this kernel (at M <= 8 a copy
+// that loaded only the x row groups below M; median error 5.5% at M = 12 and
+// 16; a fit to M = 12 and 16 alone misjudged the 3072 -> 9216 product by 20%
+// and lost its 24% gain): c plus the
 // longest of a workgroup's chain of super-tiles per wave (per round of
 // workgroups), the weight bytes at the chip's rate, the weight bytes at the
 // rate of the CUs the grid occupies, and the L2 reads (1 KiB of weights and
