@@ -248,7 +248,9 @@ int32_t mnb_max_batch_rows(void);
  * uses the context's GEMM workspace, so it must not overlap other M > 16
  * calls on the context; a group with many tiles (also one of 1 < M <= 16),
  * or whose items have M <= 64 and whose 64-row tiles balance well enough,
- * gives each workgroup whole tiles and uses no workspace.  The group keeps
+ * gives each workgroup whole tiles and uses no workspace.  An item whose x
+ * is 2 GiB or more, or whose packed weight is 4 GiB or more, is refused with
+ * MNB_ERR_UNSUPPORTED (mnb_matmul runs such x in row chunks).  The group keeps
  * its own device descriptor table, so mnb_group_run allocates nothing and can
  * be captured in a HIP graph. */
 typedef struct mnb_group mnb_group;

@@ -792,6 +792,41 @@ def test_tiny_block_scales_keep_the_bound(ctx, lo, hi):
             w16.close()
 
 
+def test_single_product_with_x_beyond_2_gib(ctx):
+    """x of one product larger than 2 GiB (M = 140000 rows at K = 8192, 2.29 GB
+    on the device): the library runs it in row chunks of at most 2 GiB
+    (131072 rows here), each planned on its own, with 32-bit offsets inside a
+    chunk.  Rows on both sides of the chunk boundary, the first and the last
+    match the oracle; the fp16 output equals the fp32 output rounded.  A group
+    refuses the same item."""
+    import torch
+    M, K, N, bs = 140000, 8192, 64, 32
+    t = synth.make_weight(9300, N, K, bs, with_zp=True)
+    w = upload(ctx, t)
+    try:
+        say("x beyond 2 GiB: plan of the first chunk", w.plan(M).as_tuple())
+        gen = torch.Generator(device="cuda").manual_seed(9301)
+        xd = torch.randn(M, K, device="cuda", generator=gen, dtype=torch.float16)
+        assert xd.numel() * 2 > (1 << 31)
+        yd = torch.empty(M, N, device="cuda", dtype=torch.float32)
+        w.matmul(xd, yd)
+        yh = torch.empty(M, N, device="cuda", dtype=torch.float16)
+        w.matmul(xd, yh)
+        torch.cuda.synchronize()
+        rows = torch.tensor([0, 1, 131070, 131071, 131072, 131073, 139998, 139999], device="cuda")
+        x16 = xd[rows].cpu().numpy()
+        y_ref, wmax = oracle_matmul(t, x16)
+        assert_parity(yd[rows].cpu().numpy(), y_ref, x16, t, wmax, False, "x beyond 2 GiB")
+        assert torch.isfinite(yd).all()
+        assert torch.equal(yh.view(torch.int16), yd.half().view(torch.int16))
+        # a group refuses such an item (its kernels take 32-bit x offsets)
+        with pytest.raises(mnb_hip.MnbError, match="x of 2 GiB or packed weights of 4 GiB or more in a group"):
+            mnb_hip.Group(ctx, [(w, xd, yd)])
+        del xd, yd, yh
+    finally:
+        w.close()
+
+
 @pytest.mark.parametrize("K", [1001, 203, 4099])
 def test_single_products_with_a_k_tail_not_a_multiple_of_8(ctx, K):
     """K % 8 != 0: the kernels read x in 16-byte pieces, so x is first copied
