@@ -190,7 +190,9 @@ int64_t mnb_weight_device_bytes(const mnb_weight *w);
  *   x_elems         number of elements the caller's x holds; M == 1 requires
  *                   x_elems == K ("Input length L != K=K"), M > 1 requires >= M*K
  *   y_elems         elements in y; must be >= M*N
- *   M               any M >= 1 (no 256-row chunking is needed)
+ *   M               any M >= 1 (no 256-row chunking is needed; x beyond 2 GiB
+ *                   runs in row chunks); with packed weights of 4 GiB or more
+ *                   only M <= 16 (else MNB_ERR_UNSUPPORTED)
  * Arithmetic: products of fp16 operands accumulated in fp32.  The output is
  * within 1e-3*sqrt(K)*max|x|*max|w| of the reference's fp32 CPU path, for any
  * block scales (the device copy of a weight's scales carries a power of two

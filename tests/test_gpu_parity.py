@@ -827,6 +827,40 @@ def test_single_product_with_x_beyond_2_gib(ctx):
         w.close()
 
 
+def test_packed_weight_of_4_gib(ctx):
+    """A weight of 4 GiB of packed nibbles (N = 524288, K = 16384, bs 32;
+    4.5 GB resident with its scales): the repack and the M <= 16 kernels use
+    64-bit offsets, so products at M = 1 and M = 4 match the oracle on output
+    columns spread over the whole weight, the last ones lying past 4 GiB.  The
+    GEMM and K-sliced kernels take 32-bit offsets into the scales: M > 16 is
+    refused with MNB_ERR_UNSUPPORTED by mnb_matmul and mnb_matmul_plan, and
+    9 <= M <= 16 stays on the GEMV."""
+    import torch
+    N, K, bs = 524288, 16384, 32
+    t = synth.make_weight(9400, N, K, bs)
+    assert t.q.nbytes == 4 << 30
+    w = upload(ctx, t)
+    try:
+        say("4 GiB weight resident: %d bytes" % w.device_bytes)
+        cols = np.concatenate([np.arange(0, N, 2053), np.arange(N - 40, N)])
+        for M in (1, 4):
+            x16 = synth.make_x(9401 + M, M, K)
+            y = w.matmul(x16)
+            y_ref, _ = oracle_matmul(t, x16, cols, want_wmax=False)
+            assert_parity(y.reshape(M, N)[:, cols], y_ref, x16, t, None, False, "4 GiB weight M=%d" % M)
+        assert w.plan(16).kernel == mnb_hip.MNB_KERNEL_GEMV, w.plan(16).as_tuple()
+        x17 = torch.zeros(17, K, device="cuda", dtype=torch.float16)
+        y17 = torch.zeros(17, N, device="cuda", dtype=torch.float16)
+        with pytest.raises(mnb_hip.MnbError, match="packed weights of 4 GiB or more run only with M <= 16"):
+            w.matmul(x17, y17)
+        with pytest.raises(mnb_hip.MnbError, match="packed weights of 4 GiB or more run only with M <= 16"):
+            w.plan(17)
+        torch.cuda.synchronize()
+        assert not torch.any(y17), "the refused call wrote y"
+    finally:
+        w.close()
+
+
 @pytest.mark.parametrize("K", [1001, 203, 4099])
 def test_single_products_with_a_k_tail_not_a_multiple_of_8(ctx, K):
     """K % 8 != 0: the kernels read x in 16-byte pieces, so x is first copied

@@ -586,6 +586,8 @@ int32_t mnb_matmul_plan(const mnb_context *ctx, const mnb_weight *w, int32_t M, 
     if (M < 1 || M > mnb_max_batch_rows()) return fail(MNB_ERR_INVALID_ARGUMENT, "M out of range [1, %d]: %d", mnb_max_batch_rows(), M);
     *out = mnb_plan_info{};
     const WeightGeom &g = w->g;
+    if (M > mnb::kSkinnyMaxM && mnb::weight_over_4gib(g))
+        return fail(MNB_ERR_UNSUPPORTED, "packed weights of 4 GiB or more run only with M <= 16 (M=%d)", M);
     if (M <= mnb::kSkinnyMaxM) {
         const mnb::KsPlan kp = mnb::ks_skinny_plan(g, M, ctx->cu_count);
         if (kp.wgs > 0) {
@@ -680,6 +682,8 @@ int32_t mnb::check_matmul(const mnb_context *ctx, const mnb_weight *w, int32_t M
         return fail(MNB_ERR_INVALID_ARGUMENT, "Input length %lld != K=%d", (long long)x_elems, g.K);
     if (x_elems < MK) return fail(MNB_ERR_INVALID_ARGUMENT, "xBatch too short: %lld < %lld", (long long)x_elems, (long long)MK);
     if (y_elems < MN) return fail(MNB_ERR_INVALID_ARGUMENT, "outBatch too short: %lld < %lld", (long long)y_elems, (long long)MN);
+    if (M > mnb::kSkinnyMaxM && mnb::weight_over_4gib(g))
+        return fail(MNB_ERR_UNSUPPORTED, "packed weights of 4 GiB or more run only with M <= 16 (M=%d)", M);
     return MNB_OK;
 }
 
@@ -828,7 +832,7 @@ static int32_t group_create_gemm(mnb_context *ctx, int32_t count, const mnb_grou
         } else if (plan.scale_f32 != g.scale_f32 || plan.has_zp != g.has_zp || plan.sps != g.SPS) {
             return fail(MNB_ERR_UNSUPPORTED, "item %d: a group needs one weight variant and one M class", i);
         }
-        if ((int64_t)it.M * g.K * 2 >= ((int64_t)1 << 31) || (uint64_t)g.NT * (uint64_t)g.ST * mnb::kTileBytes >= ((uint64_t)1 << 32))
+        if ((int64_t)it.M * g.K * 2 >= ((int64_t)1 << 31) || mnb::weight_over_4gib(g))
             return fail(MNB_ERR_UNSUPPORTED, "item %d: x of 2 GiB or packed weights of 4 GiB or more in a group", i);
         mnb::MatmulArgs &a = args[(size_t)i];
         a.x = (const _Float16 *)it.x;

@@ -60,6 +60,13 @@ struct WeightGeom {
     int32_t fold_exp = 0;         // stored scales = scales * 2^fold_exp
 };
 
+// Packed weights of 4 GiB or more: the GEMM and K-sliced kernels address the
+// scales and zero points with 32-bit offsets, so such weights run only on
+// the M <= 16 kernels (64-bit offsets).
+inline bool weight_over_4gib(const WeightGeom &g) {
+    return (uint64_t)g.NT * (uint64_t)g.ST * (uint64_t)kTileBytes >= ((uint64_t)1 << 32);
+}
+
 WeightGeom make_geom(int32_t N, int32_t K, int32_t bs);
 
 // 2^e as a float, -126 <= e <= 127 (exact).
