@@ -244,8 +244,10 @@ int32_t mnb_max_batch_rows(void);
  * Each item: device pointers, fp16 x [M, K] (K a multiple of 8, 16-byte
  * aligned), y [M, N] fp16 or fp32, M >= 1; all items share the weight variant
  * (scale type, zero points or not, block size class) and one M class: all
- * M == 1 (one persistent streaming launch), all 1 < M <= 16, or all M > 16
- * (prefill-shaped products: one GEMM launch over all items' tiles).  A GEMM
+ * M == 1 (one persistent streaming launch), all 1 < M <= 16 (when no item
+ * has more than 4 rows, the streaming launch with 2 or 4 rows of x per job),
+ * or all M > 16 (prefill-shaped products: one GEMM launch over all items'
+ * tiles).  A GEMM
  * group with few tiles splits tiles across workgroups (stream-K) and then
  * uses the context's GEMM workspace, so it must not overlap other M > 16
  * calls on the context; a group with many tiles (also one of 1 < M <= 16),
@@ -275,8 +277,8 @@ int32_t mnb_group_destroy(mnb_group *group);
  * reference counterpart: the schedule is chosen by cost models, and this
  * lets callers and tests see the choice). */
 #define MNB_KERNEL_GEMV 1        /* one workgroup per 16-row n-tile, waves split K (M <= 16) */
-#define MNB_KERNEL_STREAM 2      /* persistent weight stream over (product, n-tile) units (M == 1 groups) */
-#define MNB_KERNEL_GEMV_GROUP 3  /* the GEMV kernel over every product's n-tiles (1 < M <= 16 groups) */
+#define MNB_KERNEL_STREAM 2      /* persistent weight stream over (product, n-tile) units (groups with M <= 4) */
+#define MNB_KERNEL_GEMV_GROUP 3  /* the GEMV kernel over every product's n-tiles (4 < M <= 16 groups) */
 #define MNB_KERNEL_GEMM 4        /* the MFMA GEMM */
 #define MNB_KERNEL_KSLICE 5      /* one product, M >= 9: workgroup per output block, its waves split K (no split tiles) */
 #define MNB_ORDER_NONE 0         /* one unit of work per workgroup or a static unit list */
@@ -285,7 +287,8 @@ int32_t mnb_group_destroy(mnb_group *group);
 typedef struct mnb_plan_info {
     int32_t kernel;      /* MNB_KERNEL_* */
     int32_t order;       /* MNB_ORDER_* */
-    int32_t tile_rows;   /* output tile: rows of x (GEMM 32, 64 or 128; K-sliced 16 (M <= 16), 32, 64 or 128); 0 otherwise */
+    int32_t tile_rows;   /* output tile: rows of x (GEMM 32, 64 or 128; K-sliced 16 (M <= 16), 32, 64 or 128;
+                            streaming kernel 2 or 4 for groups with 2 <= M <= 4); 0 otherwise */
     int32_t tile_cols;   /* output tile: columns (GEMM 256 or 512; K-sliced 16, 32 or 64); 16 for the GEMV kernels */
     int32_t workgroups;  /* grid size */
 } mnb_plan_info;

@@ -6,7 +6,8 @@ and the batched recording of WarpExecutionContext.java:131-160).
 Products on device pointers allocate nothing and record only kernel launches,
 so a sequence of them -- single-row products, a prefill product whose tiles
 are split over workgroups (GEMM plus its reduce kernel), a prefill product
-on the K-sliced kernel, and a group launch -- is captured into a HIP graph on
+on the K-sliced kernel, and group launches (M = 1, and a 3-row group on the
+streaming kernel) -- is captured into a HIP graph on
 a fresh context, with no eager call first.
 Each replay, with new activations written by eager work between replays,
 equals the eager calls bit for bit."""
@@ -46,12 +47,14 @@ def test_graph_capture_replays_match_eager():
         xk = torch.empty(200, 3072, device=dev, dtype=torch.float16)
         x12 = torch.empty(12, 3072, device=dev, dtype=torch.float16)
         xg = [torch.empty(576, device=dev, dtype=torch.float16) for _ in w_g]
+        xg3 = [torch.empty(3, 576, device=dev, dtype=torch.float16) for _ in w_g]   # small-batch group, 3 rows
         y_o = torch.empty(3072, device=dev, dtype=torch.float16)
         y_gu = torch.empty(16384, device=dev, dtype=torch.float32)
         y_pf = torch.empty(200, 9001, device=dev, dtype=torch.float16)
         y_ks = torch.empty(200, 1000, device=dev, dtype=torch.float32)
         y_k16 = torch.empty(12, 16384, device=dev, dtype=torch.float16)
         y_g = [torch.empty(1536, device=dev, dtype=torch.float16) for _ in w_g]
+        y_g3 = [torch.empty(3, 1536, device=dev, dtype=torch.float32) for _ in w_g]
         st = torch.cuda.Stream()
 
         def fill():
@@ -61,11 +64,15 @@ def test_graph_capture_replays_match_eager():
             x12.copy_(torch.randn(12, 3072, device=dev, generator=gen).half())
             for x in xg:
                 x.copy_(torch.randn(576, device=dev, generator=gen).half())
+            for x in xg3:
+                x.copy_(torch.randn(3, 576, device=dev, generator=gen).half())
 
         with torch.cuda.stream(st):
             fill()
         torch.cuda.synchronize()
         group = mnb_hip.Group(ctx, list(zip(w_g, xg, y_g)))
+        group3 = mnb_hip.Group(ctx, list(zip(w_g, xg3, y_g3)))
+        assert group3.plan().as_tuple() == (mnb_hip.MNB_KERNEL_STREAM, mnb_hip.MNB_ORDER_NONE, 4, 16)
 
         def record():
             w_o.matmul(x1, y_o, stream=st.cuda_stream)
@@ -74,13 +81,14 @@ def test_graph_capture_replays_match_eager():
             w_ks.matmul(xk, y_ks, stream=st.cuda_stream)
             w_k16.matmul(x12, y_k16, stream=st.cuda_stream)
             group.run(st.cuda_stream)
+            group3.run(st.cuda_stream)
 
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=st):
             record()
         torch.cuda.synchronize()
 
-        outs = [y_o, y_gu, y_pf, y_ks, y_k16] + y_g
+        outs = [y_o, y_gu, y_pf, y_ks, y_k16] + y_g + y_g3
         for rep in range(4):
             with torch.cuda.stream(st):
                 fill()
@@ -99,6 +107,7 @@ def test_graph_capture_replays_match_eager():
                 assert torch.equal(a.view(torch.int16) if a.dtype == torch.float16 else a.view(torch.int32),
                                    b.view(torch.int16) if b.dtype == torch.float16 else b.view(torch.int32)), (rep, i)
         group.close()
+        group3.close()
         for w in [w_o, w_gu, w_pf, w_ks, w_k16] + w_g:
             w.close()
         del graph

@@ -15,7 +15,9 @@ matmul, directml-inference/.../phi3/Phi3Weights.java:123-192):
 * the prefill step at M in {16, 128, 512, 2048} as one group launch: every
   output of every product against that product's own single launch (another
   kernel schedule), and sampled rows and columns against the oracle;
-* the Qwen2.5-0.5B step at M = 1 and 64 as one group launch.
+* the Qwen2.5-0.5B step at M = 1 and 64 as one group launch;
+* the Phi-3-mini step with M = 2 and 4 rows per product (small-batch decode)
+  as one group launch, sampled outputs of every product against the oracle.
 
 Each group output buffer is filled with NaN before the launch, so a unit or
 tile that the schedule skipped shows up as NaN; a second launch must
@@ -124,6 +126,30 @@ def test_config1_decode_step_as_one_group_launch(ctx, phi3):
     x16, xd, yd = _decode_inputs(projs, 30_000)
     ys = _run_group_twice(ctx, list(zip(ws, xd, yd)), torch.cuda.Stream())
     _check_decode_outputs(projs, host, wmax, ys, x16, "decode group")
+
+
+@pytest.mark.parametrize("M", [2, 4])
+def test_small_batch_decode_step_as_one_group_launch(ctx, phi3, M):
+    """The 129 products of the Phi-3-mini step with M = 2 and 4 rows each
+    (small-batch decode) as one group launch of the streaming kernel with M x
+    rows per job: every row of 512 sampled outputs of every product against
+    the oracle, every output written, the replay bitwise identical."""
+    import torch
+    projs, host, ws, wmax = phi3
+    x16 = [synth.make_x(32_000 + 200 * M + i, M, K) for i, (_, _, K, _) in enumerate(projs)]
+    xd = [torch.from_numpy(x).cuda() for x in x16]
+    yd = [torch.empty((M, N), dtype=torch.float16, device="cuda") for (_, _, _, N) in projs]
+    g = mnb_hip.Group(ctx, list(zip(ws, xd, yd)))
+    plan = g.plan().as_tuple()
+    g.close()
+    assert plan == (mnb_hip.MNB_KERNEL_STREAM, mnb_hip.MNB_ORDER_NONE, M, 16), plan
+    ys = _run_group_twice(ctx, list(zip(ws, xd, yd)), torch.cuda.Stream())
+    for i, ((name, layer, K, N), t, yg, x) in enumerate(zip(projs, host, ys, x16)):
+        y = yg.cpu().numpy()
+        assert not np.isnan(y).any(), "item %d (%s layer %d): outputs never written" % (i, name, layer)
+        cols = np.sort(np.random.default_rng(i).choice(N, min(N, 512), replace=False))
+        y_ref, _ = oracle_matmul(t, x, cols, want_wmax=False)
+        assert_parity(y[:, cols], y_ref, x, t, wmax[i], True, "M=%d group item %d %s.%d" % (M, i, name, layer))
 
 
 def test_config1_decode_step_as_separate_launches(ctx, phi3):

@@ -524,6 +524,7 @@ def test_group_matches_oracle_and_single_launches(ctx):
 
 
 GEMM, GEMV_GROUP, KSLICE = mnb_hip.MNB_KERNEL_GEMM, mnb_hip.MNB_KERNEL_GEMV_GROUP, mnb_hip.MNB_KERNEL_KSLICE
+STREAM = mnb_hip.MNB_KERNEL_STREAM
 STREAM_K, TILE_LIST, NO_ORDER = mnb_hip.MNB_ORDER_STREAM_K, mnb_hip.MNB_ORDER_TILE_LIST, mnb_hip.MNB_ORDER_NONE
 
 
@@ -653,19 +654,70 @@ def test_random_prefill_groups(ctx, seed):
         w.close()
 
 
-@pytest.mark.parametrize("ms", [(3, 2), (6, 3), (13, 2, 8)])
+@pytest.mark.parametrize("ms", [(6, 3), (13, 2, 8), (8, 5)])
 def test_small_groups_of_multi_row_products(ctx, ms):
-    """Groups with 1 < M <= 16 and few 32 x 512 tiles run one workgroup per
-    n-tile of each item; the x row groups loaded follow the largest M of the
-    group (one group of four rows up to M = 4, two up to 8, four above), and
-    items with fewer rows still drop their rows past M.  K tails, N tails,
-    fp16 and fp32 outputs, and a group with y +=."""
+    """Groups with 4 < M <= 16 (largest M of the group) and few 32 x 512
+    tiles run one workgroup per n-tile of each item; the x row groups loaded
+    follow the largest M of the group (two groups of four rows up to M = 8,
+    four above), and items with fewer rows still drop their rows past M.  K
+    tails, N tails, fp16 and fp32 outputs, and a group with y +=."""
     shapes = [(3072, 3072, np.float16), (1000, 500, np.float32), (8192, 700, np.float16)]
     specs = [(M, K, N, ydt, False) for M, (K, N, ydt) in zip(ms, shapes)]
-    specs.append((ms[-1], 2048, 300, np.float32, True))
+    specs.append((ms[0], 2048, 300, np.float32, True))   # M > 4: the GEMV group kernel
     assert sum((N + 511) // 512 for M, K, N, _, _ in specs) < 1024
     for w, _, _ in _check_prefill_group(ctx, specs, 2500 + sum(ms), plan=(GEMV_GROUP, NO_ORDER, 0, 16)):
         w.close()
+
+
+@pytest.mark.parametrize("bs", [16, 32, 128])
+@pytest.mark.parametrize("ms", [(2, 2, 2), (4, 3, 2)])
+def test_small_batch_groups_on_the_streaming_kernel(ctx, bs, ms):
+    """Groups whose items all have 2 <= M <= 4 rows (small-batch decode) run
+    the persistent streaming kernel with 2 or 4 x rows per job (rows past an
+    item's M re-read its last row and are never stored): zero points, bs 16
+    (two scale blocks per 32-k step), 32 and 128 (one scale per super-tile),
+    a K tail inside the last super-tile and one inside the last 4-super-tile
+    job, N tails, fp16 and fp32 outputs, and a group with y +=; each item
+    against the oracle and its own single launch, replays bitwise identical."""
+    rows = 2 if max(ms) <= 2 else 4
+    shapes = [(3072, 1000, np.float16), (1000, 130, np.float32), (8192, 700, np.float16)]
+    specs = [(M, K, N, ydt, False) for M, (K, N, ydt) in zip(ms, shapes)]
+    specs += [(ms[0], 896, 1152, np.float16, True), (ms[-1], 2048, 300, np.float32, True)]
+    for w, _, _ in _check_prefill_group(ctx, specs, 2900 + bs + sum(ms), bs=bs, plan=(STREAM, NO_ORDER, rows, 16)):
+        w.close()
+
+
+def test_small_batch_group_with_fp32_scales(ctx):
+    """The streaming kernel with 4 x rows per job on weights whose scales
+    fp16 cannot hold (the device keeps fp32 scales): items of M = 3 and 4
+    against the oracle with those scales."""
+    import torch
+    items, checks = [], []
+    for i, (M, K, N) in enumerate([(3, 3072, 777), (4, 1024, 2048)]):
+        t = synth.make_weight(9500 + i, N, K, 32)
+        s32 = t.scales_f16.astype(np.float32) * np.float32(1.0 + 2.0 ** -14)
+        w = mnb_hip.Weight(ctx, N, K, 32, t.q, s32)
+        x16 = synth.make_x(9510 + i, M, K)
+        y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+        items.append((w, torch.from_numpy(x16).cuda(), y))
+        checks.append((t, s32, x16))
+    g = mnb_hip.Group(ctx, items)
+    try:
+        assert g.plan().as_tuple() == (STREAM, NO_ORDER, 4, 16), g.plan().as_tuple()
+        g.run()
+        torch.cuda.synchronize()
+        for (w, xd, y), (t, s32, x16) in zip(items, checks):
+            kb = t.kb
+            z = synth.zp_row_padded_to_flat(np.full((t.N, (kb + 1) // 2), 0x88, np.uint8), t.N, kb)
+            xp = np.zeros((x16.shape[0], kb * 32), np.float32)
+            xp[:, :t.K] = x16.astype(np.float32)
+            y_ref = orc.matmul(t.q, s32, z, t.N, kb * 32, 32, xp, threads=THREADS)
+            wmax = float(np.abs(s32).max()) * 8.0
+            assert_parity(y.cpu().numpy(), y_ref, x16, t, wmax, False, "stream rows fp32 scales M=%d" % x16.shape[0])
+    finally:
+        g.close()
+        for w, _, _ in items:
+            w.close()
 
 
 def test_group_of_products_with_64_row_tiles(ctx):

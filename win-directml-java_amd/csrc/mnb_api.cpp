@@ -1009,10 +1009,15 @@ int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *
         plan.max_m = std::max(plan.max_m, it.M);
     }
     if (items[0].M > mnb::kSkinnyMaxM) return group_create_gemm(ctx, count, items, out);
-    // 1 < M <= 16 with many 32 x 512 tiles: the GEMM's weight stream (x
+    // M == 1, and 2 <= M <= 4 (small-batch decode): the persistent streaming
+    // kernel with 1, 2 or 4 x rows per job.  The Phi-3 step as one group at
+    // M = 2 / 3 / 4: 412-418 / 419-422 / 423-424 us on 32 x 512 GEMM tiles,
+    // 327-331 / 384-391 / 395-401 us on the streaming kernel.
+    plan.stream_rows = plan.m1 ? 1 : plan.max_m <= 2 ? 2 : plan.max_m <= 4 ? 4 : 0;
+    // 4 < M <= 16 with many 32 x 512 tiles: the GEMM's weight stream (x
     // shared by the workgroup's waves in LDS, persistent workgroups) beats one
     // workgroup per n-tile, whose waves each read their own x rows.
-    if (!plan.m1 && mnb::sk_wide_supported(plan.scale_f32, plan.sps)) {
+    if (plan.stream_rows == 0 && mnb::sk_wide_supported(plan.scale_f32, plan.sps)) {
         int64_t skinny_tiles = 0;
         for (int32_t i = 0; i < count; ++i)
             skinny_tiles += mnb::sk_tiles(items[i].M, items[i].weight->g.NT, mnb::kGemmWideNTW, mnb::kGemmSkinnyFM);
@@ -1029,15 +1034,15 @@ int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *
     plan.total_wgs = (int32_t)wgs;
     DeviceGuard guard(ctx->device);
 
-    // M == 1: static schedule for the persistent streaming kernel (units
-    // dealt longest first to the least loaded wave, mnb_sched.cpp)
+    // static schedule for the persistent streaming kernel (units dealt
+    // longest first to the least loaded wave, mnb_sched.cpp)
     std::vector<uint32_t> units;
     std::vector<int32_t> wave_begin;
-    if (plan.m1) {
+    if (plan.stream_rows > 0) {
         for (int32_t i = 0; i < count; ++i)
             if (items[i].weight->g.NT > 65536)
                 return fail(MNB_ERR_UNSUPPORTED, "item %d: N=%d too large for a group", i, items[i].weight->g.N);
-        const int wpc = mnb::stream_kernel_waves_per_cu(plan.scale_f32, plan.has_zp, plan.sps);
+        const int wpc = mnb::stream_kernel_waves_per_cu(plan.scale_f32, plan.has_zp, plan.sps, plan.stream_rows);
         const int64_t total_waves = (int64_t)ctx->cu_count * wpc;
         plan.stream_wgs = (int32_t)(total_waves / mnb::kStreamWavesPerBlock);
         std::vector<int32_t> nt((size_t)count), st((size_t)count);
@@ -1060,7 +1065,7 @@ int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *
         (e = dev_alloc(&plan.wg_item, wg_item.size() * sizeof(uint16_t))) != hipSuccess ||
         (e = hipMemcpy(plan.items, host.data(), host.size() * sizeof(mnb::GroupItem), hipMemcpyHostToDevice)) != hipSuccess ||
         (e = hipMemcpy(plan.wg_item, wg_item.data(), wg_item.size() * sizeof(uint16_t), hipMemcpyHostToDevice)) != hipSuccess ||
-        (plan.m1 && ((e = dev_alloc(&plan.units, units.size() * sizeof(uint32_t))) != hipSuccess ||
+        (plan.stream_rows > 0 && ((e = dev_alloc(&plan.units, units.size() * sizeof(uint32_t))) != hipSuccess ||
                      (e = dev_alloc(&plan.wave_begin, wave_begin.size() * sizeof(int32_t))) != hipSuccess ||
                      (e = hipMemcpy(plan.units, units.data(), units.size() * sizeof(uint32_t), hipMemcpyHostToDevice)) != hipSuccess ||
                      (e = hipMemcpy(plan.wave_begin, wave_begin.data(), wave_begin.size() * sizeof(int32_t), hipMemcpyHostToDevice)) != hipSuccess))) {
@@ -1085,7 +1090,7 @@ int32_t mnb_group_run(mnb_context *ctx, const mnb_group *group, void *stream) {
         if (e != hipSuccess) return hip_fail(e, "matmulBatch");
         return ok();
     }
-    hipError_t e = group->plan.m1 ? mnb::launch_gemv_stream(group->plan, s) : mnb::launch_gemv_group(group->plan, s);
+    hipError_t e = group->plan.stream_rows > 0 ? mnb::launch_gemv_stream(group->plan, s) : mnb::launch_gemv_group(group->plan, s);
     if (e != hipSuccess) return hip_fail(e, "matvec");
     return ok();
 }
@@ -1100,8 +1105,9 @@ int32_t mnb_group_plan(const mnb_group *group, mnb_plan_info *out) {
         out->tile_rows = 32 * g.fm;
         out->tile_cols = 128 * g.ntw;
         out->workgroups = g.G;
-    } else if (group->plan.m1) {
+    } else if (group->plan.stream_rows > 0) {
         out->kernel = MNB_KERNEL_STREAM;
+        out->tile_rows = group->plan.stream_rows > 1 ? group->plan.stream_rows : 0;
         out->tile_cols = mnb::kTileRows;
         out->workgroups = group->plan.stream_wgs;
     } else {

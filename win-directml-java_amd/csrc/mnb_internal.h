@@ -206,14 +206,17 @@ struct GemvGroupPlan {
     int32_t count = 0, total_wgs = 0, waves = 0;
     int32_t scale_f32 = 0, has_zp = 0, sps = 0, m1 = 0;
     int32_t max_m = 0;         // largest M of the items (M > 1: x row groups to load)
-    // M == 1: persistent streaming schedule
+    // the persistent streaming kernel with this many x rows per job (1: M == 1
+    // groups; 2 or 4: groups with 2 <= M <= 4), 0: the GEMV group kernel
+    int32_t stream_rows = 0;
+    // persistent streaming schedule
     void *units = nullptr;       // device uint32_t[U]: (item << 16) | n-tile, grouped by wave
     void *wave_begin = nullptr;  // device int32_t[2 * waves + 1]: per wave its first unit and 4-super-tile job count, then the end
     int32_t stream_wgs = 0;
 };
 hipError_t launch_gemv_group(const GemvGroupPlan &g, hipStream_t stream);
 hipError_t launch_gemv_stream(const GemvGroupPlan &g, hipStream_t stream);
-int stream_kernel_waves_per_cu(int scale_f32, int has_zp, int sps);
+int stream_kernel_waves_per_cu(int scale_f32, int has_zp, int sps, int rows);
 constexpr int kStreamWavesPerBlock = 4;
 
 // n-tiles (16 rows) per wave of the GEMM: 2 (256-column tiles), or 4

@@ -2,6 +2,11 @@
 //
 // A recorded group (mnb_group_create) of independent decode projections is
 // cut into units: one unit = one 16-row n-tile of one item, over its whole K.
+// Groups of products with 2 <= M <= 4 rows (small-batch decode) run the same
+// kernel with MR = 2 or 4 rows of x per job: MR 1 KiB activation loads
+// instead of one, the rows interleaved in LDS in 16-byte chunks, and MFMA row
+// m taking x row m mod MR, so that every lane's four results are rows 0..3
+// (mod MR) of its column; lane group g stores row g.
 // Each wavefront owns a list of units (balanced by bytes on the host, see
 // mnb_sched.cpp) and streams them as jobs of kStreamJobTiles (4) consecutive
 // super-tiles through a 2-deep register pipeline that runs across unit
@@ -34,9 +39,9 @@ struct UnitRef {
     const u32x4_t *q;      // first tile of the n-tile, + lane
     const ScaleT *s;       // first scale row of the n-tile, + row r
     const uint8_t *z;      // first zero-point row of the n-tile, + row r
-    const _Float16 *x;     // activation row
+    const _Float16 *x;     // activation rows, ldx apart
     void *y;
-    int32_t ST, NJ, kx, N, nt, y_f16, accumulate;
+    int32_t ST, NJ, kx, N, nt, y_f16, accumulate, M, ldx;
     float unfold;
 };
 
@@ -60,20 +65,24 @@ __device__ __forceinline__ UnitRef<ScaleT> resolve_unit(const GroupItem *__restr
     u.nt = nt;
     u.y_f16 = p.y_f16;
     u.accumulate = p.accumulate;
+    u.M = p.M;
+    u.ldx = p.ldx;
     u.unfold = p.unfold;
     return u;
 }
 
-template <typename ScaleT, bool HAS_ZP, int SPS>
+template <typename ScaleT, bool HAS_ZP, int SPS, int MR>
 __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const GroupItem *__restrict__ items,
                                                                         const uint32_t *__restrict__ units,
                                                                         const int32_t *__restrict__ wave_begin) {
     constexpr int ZB = SPS <= 2 ? 1 : SPS / 2;
     constexpr int SB = SPS * (int)sizeof(ScaleT);               // scale bytes per row per tile
     constexpr int D = kStreamDepth;
-    // per wave: a job's activations (4 x 128 fp16), scale rows and zero-point
-    // entries (4 tiles x 16 rows each)
-    constexpr int kXB = kJT * kTileK * 2, kSB = kJT * kTileRows * SB, kZB = HAS_ZP ? kJT * kTileRows * ZB : 0;
+    static_assert(MR == 1 || MR == 2 || MR == 4, "rows of x per job");
+    // per wave: a job's activations (MR rows of 4 x 128 fp16; 16-byte chunk c
+    // of row i at (c * MR + i) * 16), scale rows and zero-point entries (4
+    // tiles x 16 rows each)
+    constexpr int kXB = MR * kJT * kTileK * 2, kSB = kJT * kTileRows * SB, kZB = HAS_ZP ? kJT * kTileRows * ZB : 0;
     constexpr int kWaveLds = kXB + kSB + kZB;
     __shared__ __align__(16) unsigned char lds_all[kStreamWaves * kWaveLds];
 
@@ -93,7 +102,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
     u32x4_t raw[D][kJT];
     ScaleT sv[D][SPS];   // lane group g: tile g's scale row r
     uint32_t zb[D];
-    u32x4_t xv[D];
+    u32x4_t xv[D][MR];   // row i: this lane's 16-byte piece of x row min(i, M - 1)
     bool xok[D];         // this lane's activation piece lies below kx (applied when it is written to LDS)
 
     // issue cursor: unit index iu, job ij
@@ -112,8 +121,11 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
         if constexpr (HAS_ZP) zb[d] = load_zp<ZB>(iref.z + (size_t)stg * kTileRows * ZB);
         else zb[d] = 0x88888888u;
         // lane l brings activations k = st0 * 128 + 8 l .. + 7 (tile l / 16)
+        // of each row (rows past M re-read row M - 1, never stored)
         const int k = st0 * kTileK + 8 * lane;
-        xv[d] = gld((const u32x4_t *)(iref.x + min(k, iref.kx - 8)));
+#pragma unroll
+        for (int i = 0; i < MR; ++i)
+            xv[d][i] = gld((const u32x4_t *)(iref.x + (size_t)min(i, iref.M - 1) * iref.ldx + min(k, iref.kx - 8)));
         xok[d] = k < iref.kx;
         if (ij + 1 < iref.NJ) {
             ++ij;
@@ -126,12 +138,15 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
     // compute cursor: unit index cu, job cj
     int cu = ubeg, cj = 0;
     UnitRef<ScaleT> cref = iref;
-    float acc = 0.f;
+    float acc[MR];
+#pragma unroll
+    for (int i = 0; i < MR; ++i) acc[i] = 0.f;
     auto compute = [&](int d) {
         // wave-private LDS: a wave's LDS accesses complete in order, and the
         // compiler barriers keep this job's writes after the previous job's
         // reads and its reads after its writes
-        *(u32x4_st_alias_t *)(xw + lane * 16) = xok[d] ? xv[d] : zero4;
+#pragma unroll
+        for (int i = 0; i < MR; ++i) *(u32x4_st_alias_t *)(xw + (lane * MR + i) * 16) = xok[d] ? xv[d][i] : zero4;
         __builtin_memcpy(sw + (gg * kTileRows + r) * SB, &sv[d][0], SB);
         if constexpr (HAS_ZP) __builtin_memcpy(zw + (gg * kTileRows + r) * ZB, &zb[d], ZB);
         asm volatile("" ::: "memory");
@@ -142,7 +157,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
             if (cj * kJT + t >= cref.ST) break;
             half8_t xa[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) xa[j] = *(const half8_st_alias_t *)(xw + t * (kTileK * 2) + (32 * j + 8 * gg) * 2);
+            for (int j = 0; j < 4; ++j)   // MFMA row r: x row r mod MR, k chunk 16 t + 4 j + gg
+                xa[j] = *(const half8_st_alias_t *)(xw + ((16 * t + 4 * j + gg) * MR + r % MR) * 16);
             ScaleT sc[SPS];
             __builtin_memcpy(&sc[0], sw + (t * kTileRows + r) * SB, SB);
             uint32_t zt = 0x88888888u;
@@ -157,7 +173,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
                     b = b * (_Float16)(float)((gg >> 1) ? sc[2 * j + 1] : sc[2 * j]);
                     dd = mfma16x16x32(xa[j], b, dd);
                 }
-                acc += dd[0];
+#pragma unroll
+                for (int q = 0; q < MR; ++q) acc[q] += dd[q];
             } else {
                 constexpr int KPB = 4 / SPS;
 #pragma unroll
@@ -170,20 +187,29 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
                         const int j = i * KPB + u;
                         dd = mfma16x16x32(xa[j], unpack_q_minus_zp(raw[d][t][j], blo, bhi, k6400), dd);
                     }
-                    acc = fmaf((float)sc[i], dd[0], acc);
+#pragma unroll
+                    for (int q = 0; q < MR; ++q) acc[q] = fmaf((float)sc[i], dd[q], acc[q]);
                 }
             }
         }
         asm volatile("" ::: "memory");
         if (++cj == cref.NJ) {
-            // x was broadcast to all 16 MFMA rows: lanes 0..15 hold row 0, column r
+            // MFMA row m used x row m mod MR, so every lane holds rows 0 .. MR - 1
+            // of its column r in acc; lane group g stores row g
+            // (one store per row with constant register indices: a select by
+            // lane would put acc in scratch memory)
             const int n = cref.nt * kTileRows + r;
-            if (gg == 0 && n < cref.N) {
-                const float v = acc * cref.unfold;   // undo the stored scales' 2^fold_exp
-                if (cref.y_f16) store_y<true>(cref.y, (size_t)n, v, cref.accumulate != 0);
-                else store_y<false>(cref.y, (size_t)n, v, cref.accumulate != 0);
+#pragma unroll
+            for (int q = 0; q < MR; ++q) {
+                if (gg == q && q < cref.M && n < cref.N) {
+                    const float v = acc[q] * cref.unfold;   // undo the stored scales' 2^fold_exp
+                    const size_t idx = (size_t)q * cref.N + n;
+                    if (cref.y_f16) store_y<true>(cref.y, idx, v, cref.accumulate != 0);
+                    else store_y<false>(cref.y, idx, v, cref.accumulate != 0);
+                }
             }
-            acc = 0.f;
+#pragma unroll
+            for (int q = 0; q < MR; ++q) acc[q] = 0.f;
             cj = 0;
             if (cu + 1 < uend) cref = resolve_unit<ScaleT, SPS, ZB>(items, units[++cu], lane, r);
         }
@@ -209,8 +235,13 @@ hipError_t launch_gemv_stream(const GemvGroupPlan &g, hipStream_t stream) {
     const GroupItem *it = (const GroupItem *)g.items;
     const uint32_t *un = (const uint32_t *)g.units;
     const int32_t *wb = (const int32_t *)g.wave_begin;
-#define MNB_STREAM_LAUNCH(ST_, ZP_, SPS_) \
-    hipLaunchKernelGGL((gemv_stream_kernel<ST_, ZP_, SPS_>), grid, block, 0, stream, it, un, wb)
+    if (g.stream_rows != 1 && g.stream_rows != 2 && g.stream_rows != 4) return hipErrorInvalidValue;
+#define MNB_STREAM_MR(ST_, ZP_, SPS_, MR_) \
+    hipLaunchKernelGGL((gemv_stream_kernel<ST_, ZP_, SPS_, MR_>), grid, block, 0, stream, it, un, wb)
+#define MNB_STREAM_LAUNCH(ST_, ZP_, SPS_)                                       \
+    if (g.stream_rows == 1) { MNB_STREAM_MR(ST_, ZP_, SPS_, 1); }              \
+    else if (g.stream_rows == 2) { MNB_STREAM_MR(ST_, ZP_, SPS_, 2); }         \
+    else { MNB_STREAM_MR(ST_, ZP_, SPS_, 4); }
 #define MNB_STREAM_SPS(ST_, ZP_)                               \
     switch (g.sps) {                                           \
         case 1: MNB_STREAM_LAUNCH(ST_, ZP_, 1); break;         \
@@ -226,14 +257,19 @@ hipError_t launch_gemv_stream(const GemvGroupPlan &g, hipStream_t stream) {
     }
 #undef MNB_STREAM_SPS
 #undef MNB_STREAM_LAUNCH
+#undef MNB_STREAM_MR
     return hipGetLastError();
 }
 
-int stream_kernel_waves_per_cu(int scale_f32, int has_zp, int sps) {
+int stream_kernel_waves_per_cu(int scale_f32, int has_zp, int sps, int rows) {
     int blocks = 0;
     hipError_t e = hipSuccess;
-#define MNB_OCC(ST_, ZP_, SPS_) \
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, gemv_stream_kernel<ST_, ZP_, SPS_>, 64 * kStreamWaves, 0)
+#define MNB_OCC_MR(ST_, ZP_, SPS_, MR_) \
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, gemv_stream_kernel<ST_, ZP_, SPS_, MR_>, 64 * kStreamWaves, 0)
+#define MNB_OCC(ST_, ZP_, SPS_)                                  \
+    if (rows == 1) { MNB_OCC_MR(ST_, ZP_, SPS_, 1); }            \
+    else if (rows == 2) { MNB_OCC_MR(ST_, ZP_, SPS_, 2); }       \
+    else { MNB_OCC_MR(ST_, ZP_, SPS_, 4); }
 #define MNB_OCC_SPS(ST_, ZP_)                  \
     switch (sps) {                             \
         case 1: MNB_OCC(ST_, ZP_, 1); break;   \
@@ -248,6 +284,7 @@ int stream_kernel_waves_per_cu(int scale_f32, int has_zp, int sps) {
     }
 #undef MNB_OCC_SPS
 #undef MNB_OCC
+#undef MNB_OCC_MR
     if (e != hipSuccess || blocks < 1) blocks = 1;
     return blocks * kStreamWaves;
 }
