@@ -19,6 +19,8 @@ M=512, Phi-3-mini shapes"):
   stream order.
 * roofline: per-launch HIP-event timing of the dominant kernel (the M=1
   kernel) and of the M=512 kernel, against 8 TB/s HBM and 2.5 PFLOP/s fp16.
+* small_batch_decode: the same 129 projections with 2 and 4 rows each (a
+  decode step of 2 or 4 sequences) as one group launch.
 * config0: the single qkv product (M=1) as back-to-back launches over 17
   weight copies (each launch reads from HBM).
 * qwen: the Qwen2.5-0.5B tied lm_head (quantized on the device, M=1) and the
@@ -683,6 +685,16 @@ def main():
             torch.cuda.empty_cache()
             log("prefill M=%d: %.1f TFLOP/s as one group launch, %.1f as 129 launches" % (
                 M, sweep[str(M)], sweep_seq[str(M)]))
+    # small-batch decode: the 129 projections with 2 and 4 rows each as one
+    # group launch (the streaming kernel with 2 or 4 activation rows per job)
+    small_batch = {}
+    for M in (2, 4):
+        _, fl, w_m, _ = prefill(M, group=True)
+        nb = sum(t.algorithmic_bytes(M) for t in host)
+        small_batch[str(M)] = {"us_per_step": round(w_m * 1e6, 1), "gbs": round(nb / w_m / 1e9, 1),
+                               "bytes_per_step": nb, "tflops": round(fl / w_m / 1e12, 2)}
+        torch.cuda.empty_cache()
+        log("small-batch decode M=%d as one group launch: %.1f us, %.1f GB/s" % (M, w_m * 1e6, nb / w_m / 1e9))
 
     copy_gbs = copy_bandwidth(torch, stream)
     log("device copy bandwidth: %.0f GB/s" % copy_gbs)
@@ -766,6 +778,8 @@ def main():
                                       "traffic_source": "profiles/gemm_sk_phi3_prefill_m512.md "
                                                         "(rocprofv3 FETCH_SIZE + WRITE_SIZE)"},
                          "sweep_tflops": sweep_seq},
+        "small_batch_decode": dict(small_batch, note="the 129 projections with M rows each recorded as one group "
+                                                     "(mnb::gemv_stream_kernel with M activation rows per job)"),
         "device_copy_gbs": round(copy_gbs, 1),
         "torch_read_gbs": round(read_gbs, 1),
         "config0_single_qkv": cfg0,
