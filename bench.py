@@ -686,7 +686,7 @@ def main():
             log("prefill M=%d: %.1f TFLOP/s as one group launch, %.1f as 129 launches" % (
                 M, sweep[str(M)], sweep_seq[str(M)]))
     # small-batch decode: the 129 projections with 2 and 4 rows each as one
-    # group launch (the streaming kernel with 2 or 4 activation rows per job)
+    # group launch (the streaming kernel with M activation rows per job)
     small_batch = {}
     for M in (2, 4):
         _, fl, w_m, _ = prefill(M, group=True)

@@ -245,7 +245,8 @@ int32_t mnb_max_batch_rows(void);
  * aligned), y [M, N] fp16 or fp32, M >= 1; all items share the weight variant
  * (scale type, zero points or not, block size class) and one M class: all
  * M == 1 (one persistent streaming launch), all 1 < M <= 16 (when no item
- * has more than 4 rows, the streaming launch with 2 or 4 rows of x per job),
+ * has more than 4 rows, the streaming launch with the group's largest M rows
+ * of x per job),
  * or all M > 16 (prefill-shaped products: one GEMM launch over all items'
  * tiles).  A GEMM
  * group with few tiles splits tiles across workgroups (stream-K) and then
@@ -288,7 +289,7 @@ typedef struct mnb_plan_info {
     int32_t kernel;      /* MNB_KERNEL_* */
     int32_t order;       /* MNB_ORDER_* */
     int32_t tile_rows;   /* output tile: rows of x (GEMM 32, 64 or 128; K-sliced 16 (M <= 16), 32, 64 or 128;
-                            streaming kernel 2 or 4 for groups with 2 <= M <= 4); 0 otherwise */
+                            streaming kernel: the group's largest M when 2 <= M <= 4); 0 otherwise */
     int32_t tile_cols;   /* output tile: columns (GEMM 256 or 512; K-sliced 16, 32 or 64); 16 for the GEMV kernels */
     int32_t workgroups;  /* grid size */
 } mnb_plan_info;

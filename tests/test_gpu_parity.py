@@ -670,16 +670,17 @@ def test_small_groups_of_multi_row_products(ctx, ms):
 
 
 @pytest.mark.parametrize("bs", [16, 32, 128])
-@pytest.mark.parametrize("ms", [(2, 2, 2), (4, 3, 2)])
+@pytest.mark.parametrize("ms", [(2, 2, 2), (3, 2, 3), (4, 3, 2)])
 def test_small_batch_groups_on_the_streaming_kernel(ctx, bs, ms):
     """Groups whose items all have 2 <= M <= 4 rows (small-batch decode) run
-    the persistent streaming kernel with 2 or 4 x rows per job (rows past an
-    item's M re-read its last row and are never stored): zero points, bs 16
+    the persistent streaming kernel with as many x rows per job as the
+    group's largest M (rows past an item's M re-read its last row and are
+    never stored): zero points, bs 16
     (two scale blocks per 32-k step), 32 and 128 (one scale per super-tile),
     a K tail inside the last super-tile and one inside the last 4-super-tile
     job, N tails, fp16 and fp32 outputs, and a group with y +=; each item
     against the oracle and its own single launch, replays bitwise identical."""
-    rows = 2 if max(ms) <= 2 else 4
+    rows = max(ms)
     shapes = [(3072, 1000, np.float16), (1000, 130, np.float32), (8192, 700, np.float16)]
     specs = [(M, K, N, ydt, False) for M, (K, N, ydt) in zip(ms, shapes)]
     specs += [(ms[0], 896, 1152, np.float16, True), (ms[-1], 2048, 300, np.float32, True)]

@@ -1010,10 +1010,8 @@ int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *
     }
     if (items[0].M > mnb::kSkinnyMaxM) return group_create_gemm(ctx, count, items, out);
     // M == 1, and 2 <= M <= 4 (small-batch decode): the persistent streaming
-    // kernel with 1, 2 or 4 x rows per job.  The Phi-3 step as one group at
-    // M = 2 / 3 / 4: 412-418 / 419-422 / 423-424 us on 32 x 512 GEMM tiles,
-    // 327-331 / 384-391 / 395-401 us on the streaming kernel.
-    plan.stream_rows = plan.m1 ? 1 : plan.max_m <= 2 ? 2 : plan.max_m <= 4 ? 4 : 0;
+    // kernel with as many x rows per job as the group's largest M.
+    plan.stream_rows = plan.m1 ? 1 : plan.max_m <= 4 ? plan.max_m : 0;
     // 4 < M <= 16 with many 32 x 512 tiles: the GEMM's weight stream (x
     // shared by the workgroup's waves in LDS, persistent workgroups) beats one
     // workgroup per n-tile, whose waves each read their own x rows.

@@ -207,7 +207,8 @@ struct GemvGroupPlan {
     int32_t scale_f32 = 0, has_zp = 0, sps = 0, m1 = 0;
     int32_t max_m = 0;         // largest M of the items (M > 1: x row groups to load)
     // the persistent streaming kernel with this many x rows per job (1: M == 1
-    // groups; 2 or 4: groups with 2 <= M <= 4), 0: the GEMV group kernel
+    // groups; 2 to 4: the largest M of groups with 2 <= M <= 4), 0: the GEMV
+    // group kernel
     int32_t stream_rows = 0;
     // persistent streaming schedule
     void *units = nullptr;       // device uint32_t[U]: (item << 16) | n-tile, grouped by wave

@@ -3,10 +3,11 @@
 // A recorded group (mnb_group_create) of independent decode projections is
 // cut into units: one unit = one 16-row n-tile of one item, over its whole K.
 // Groups of products with 2 <= M <= 4 rows (small-batch decode) run the same
-// kernel with MR = 2 or 4 rows of x per job: MR 1 KiB activation loads
-// instead of one, the rows interleaved in LDS in 16-byte chunks, and MFMA row
-// m taking x row m mod MR, so that every lane's four results are rows 0..3
-// (mod MR) of its column; lane group g stores row g.
+// kernel with MR = M rows of x per job: MR 1 KiB activation loads instead of
+// one, the rows interleaved in LDS in 16-byte chunks, and MFMA row m taking x
+// row min(m / 4, MR - 1), so that lane group g's four results all belong to
+// x row g: each lane keeps one sum, as for M = 1, and lane group g stores row
+// g.
 // Each wavefront owns a list of units (balanced by bytes on the host, see
 // mnb_sched.cpp) and streams them as jobs of kStreamJobTiles (4) consecutive
 // super-tiles through a 2-deep register pipeline that runs across unit
@@ -78,7 +79,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
     constexpr int ZB = SPS <= 2 ? 1 : SPS / 2;
     constexpr int SB = SPS * (int)sizeof(ScaleT);               // scale bytes per row per tile
     constexpr int D = kStreamDepth;
-    static_assert(MR == 1 || MR == 2 || MR == 4, "rows of x per job");
+    static_assert(MR >= 1 && MR <= 4, "rows of x per job");
     // per wave: a job's activations (MR rows of 4 x 128 fp16; 16-byte chunk c
     // of row i at (c * MR + i) * 16), scale rows and zero-point entries (4
     // tiles x 16 rows each)
@@ -138,9 +139,9 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
     // compute cursor: unit index cu, job cj
     int cu = ubeg, cj = 0;
     UnitRef<ScaleT> cref = iref;
-    float acc[MR];
-#pragma unroll
-    for (int i = 0; i < MR; ++i) acc[i] = 0.f;
+    float acc = 0.f;
+    // x row of MFMA row r (A operand): lane group g's results are MFMA rows 4 g .. 4 g + 3
+    const int xrow = MR == 1 ? 0 : min(r >> 2, MR - 1);
     auto compute = [&](int d) {
         // wave-private LDS: a wave's LDS accesses complete in order, and the
         // compiler barriers keep this job's writes after the previous job's
@@ -157,8 +158,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
             if (cj * kJT + t >= cref.ST) break;
             half8_t xa[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)   // MFMA row r: x row r mod MR, k chunk 16 t + 4 j + gg
-                xa[j] = *(const half8_st_alias_t *)(xw + ((16 * t + 4 * j + gg) * MR + r % MR) * 16);
+            for (int j = 0; j < 4; ++j)   // MFMA row r: x row xrow, k chunk 16 t + 4 j + gg
+                xa[j] = *(const half8_st_alias_t *)(xw + ((16 * t + 4 * j + gg) * MR + xrow) * 16);
             ScaleT sc[SPS];
             __builtin_memcpy(&sc[0], sw + (t * kTileRows + r) * SB, SB);
             uint32_t zt = 0x88888888u;
@@ -173,8 +174,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
                     b = b * (_Float16)(float)((gg >> 1) ? sc[2 * j + 1] : sc[2 * j]);
                     dd = mfma16x16x32(xa[j], b, dd);
                 }
-#pragma unroll
-                for (int q = 0; q < MR; ++q) acc[q] += dd[q];
+                acc += dd[0];
             } else {
                 constexpr int KPB = 4 / SPS;
 #pragma unroll
@@ -187,29 +187,22 @@ __global__ __launch_bounds__(64 * kStreamWaves) void gemv_stream_kernel(const Gr
                         const int j = i * KPB + u;
                         dd = mfma16x16x32(xa[j], unpack_q_minus_zp(raw[d][t][j], blo, bhi, k6400), dd);
                     }
-#pragma unroll
-                    for (int q = 0; q < MR; ++q) acc[q] = fmaf((float)sc[i], dd[q], acc[q]);
+                    acc = fmaf((float)sc[i], dd[0], acc);
                 }
             }
         }
         asm volatile("" ::: "memory");
         if (++cj == cref.NJ) {
-            // MFMA row m used x row m mod MR, so every lane holds rows 0 .. MR - 1
-            // of its column r in acc; lane group g stores row g
-            // (one store per row with constant register indices: a select by
-            // lane would put acc in scratch memory)
+            // lane group g holds x row g (for M = 1 every group holds row 0):
+            // group g stores row g of its column r
             const int n = cref.nt * kTileRows + r;
-#pragma unroll
-            for (int q = 0; q < MR; ++q) {
-                if (gg == q && q < cref.M && n < cref.N) {
-                    const float v = acc[q] * cref.unfold;   // undo the stored scales' 2^fold_exp
-                    const size_t idx = (size_t)q * cref.N + n;
-                    if (cref.y_f16) store_y<true>(cref.y, idx, v, cref.accumulate != 0);
-                    else store_y<false>(cref.y, idx, v, cref.accumulate != 0);
-                }
+            if (gg < MR && gg < cref.M && n < cref.N) {
+                const float v = acc * cref.unfold;   // undo the stored scales' 2^fold_exp
+                const size_t idx = (size_t)gg * cref.N + n;
+                if (cref.y_f16) store_y<true>(cref.y, idx, v, cref.accumulate != 0);
+                else store_y<false>(cref.y, idx, v, cref.accumulate != 0);
             }
-#pragma unroll
-            for (int q = 0; q < MR; ++q) acc[q] = 0.f;
+            acc = 0.f;
             cj = 0;
             if (cu + 1 < uend) cref = resolve_unit<ScaleT, SPS, ZB>(items, units[++cu], lane, r);
         }
@@ -235,12 +228,13 @@ hipError_t launch_gemv_stream(const GemvGroupPlan &g, hipStream_t stream) {
     const GroupItem *it = (const GroupItem *)g.items;
     const uint32_t *un = (const uint32_t *)g.units;
     const int32_t *wb = (const int32_t *)g.wave_begin;
-    if (g.stream_rows != 1 && g.stream_rows != 2 && g.stream_rows != 4) return hipErrorInvalidValue;
+    if (g.stream_rows < 1 || g.stream_rows > 4) return hipErrorInvalidValue;
 #define MNB_STREAM_MR(ST_, ZP_, SPS_, MR_) \
     hipLaunchKernelGGL((gemv_stream_kernel<ST_, ZP_, SPS_, MR_>), grid, block, 0, stream, it, un, wb)
 #define MNB_STREAM_LAUNCH(ST_, ZP_, SPS_)                                       \
     if (g.stream_rows == 1) { MNB_STREAM_MR(ST_, ZP_, SPS_, 1); }              \
     else if (g.stream_rows == 2) { MNB_STREAM_MR(ST_, ZP_, SPS_, 2); }         \
+    else if (g.stream_rows == 3) { MNB_STREAM_MR(ST_, ZP_, SPS_, 3); }         \
     else { MNB_STREAM_MR(ST_, ZP_, SPS_, 4); }
 #define MNB_STREAM_SPS(ST_, ZP_)                               \
     switch (g.sps) {                                           \
@@ -269,6 +263,7 @@ int stream_kernel_waves_per_cu(int scale_f32, int has_zp, int sps, int rows) {
 #define MNB_OCC(ST_, ZP_, SPS_)                                  \
     if (rows == 1) { MNB_OCC_MR(ST_, ZP_, SPS_, 1); }            \
     else if (rows == 2) { MNB_OCC_MR(ST_, ZP_, SPS_, 2); }       \
+    else if (rows == 3) { MNB_OCC_MR(ST_, ZP_, SPS_, 3); }       \
     else { MNB_OCC_MR(ST_, ZP_, SPS_, 4); }
 #define MNB_OCC_SPS(ST_, ZP_)                  \
     switch (sps) {                             \
