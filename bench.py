@@ -578,10 +578,11 @@ def main():
 
 
     if args.phase == "prefill":
-        _, fl, w_m, _ = prefill(args.prefill_m, group=args.prefill_group)
+        _, fl, w_m, g_m = prefill(args.prefill_m, group=args.prefill_group)
         print(json.dumps({"phase": "prefill", "M": args.prefill_m, "group": args.prefill_group,
                           "tflops": round(fl / w_m / 1e12, 2),
-                          "us_per_step": round(w_m * 1e6, 1), "flops_per_step": fl}), flush=True)
+                          "us_per_step": round(w_m * 1e6, 1), "gpu_us_per_step": round(g_m * 1e6, 1),
+                          "flops_per_step": fl}), flush=True)
         for w in weights:
             w.close()
         ctx.close()
@@ -744,9 +745,11 @@ def main():
                      "avg_launch_us": round(kern * 1e6, 2)},
         "decode_step_sequential": {"gbs": round(bytes_step / wall_seq / 1e9, 2),
                                    "ms_per_step": round(wall_seq * 1e3, 4),
+                                   "gpu_ms_per_step": round(gpu_seq * 1e3, 4),
                                    "frac_hbm_peak": round(bytes_step / wall_seq / 1e9 / HBM_PEAK_GBS, 4),
                                    "note": "the same 129 projections as 129 stream-ordered launches "
-                                           "(mnb::gemv_kernel, HIP graph)",
+                                           "(mnb::gemv_kernel, HIP graph); gpu_ms_per_step is the span of "
+                                           "HIP events around the replays on the launch stream",
                                    "per_shape": per_shape},
         "prefill_m512": {"tflops": round(tflops512, 2), "ms_per_step": round(wall512 * 1e3, 4),
                          "flops_per_step": flops512, "frac_fp16_peak": round(tflops512 / FP16_PEAK_TFLOPS, 4),

@@ -142,10 +142,12 @@ def test_config4_asymmetric_tails(ctx, M, bs, K, N):
 
 @pytest.mark.parametrize("M", [2, 3, 4, 6, 8, 9, 12, 16])
 def test_multi_row_products_by_row_group(ctx, M):
-    """Single products with 1 < M <= 16 load the x rows in groups of four
-    (one group up to M = 4, two up to 8, four above); rows past M feed
-    discarded results.  Shapes: whole super-tiles, a K tail with zero points
-    and fp32 scales, and K = 8192, where 12 waves loop over 32 K chunks."""
+    """Single products with 1 < M <= 16 load the x rows in XR groups of four
+    (XR = 1 up to M = 4, 2 up to 8, 4 above) and MFMA row m reads x row
+    m * XR / 4, so with M <= 4 a lane keeps one sum per output row, with
+    M <= 8 two; rows past M repeat row M - 1 and are not stored.  Shapes:
+    whole super-tiles, a K tail with zero points and fp32 scales, and
+    K = 8192, where 12 waves loop over 32 K chunks."""
     cases = [(3072, 200, 32, False, False), (1000, 130, 128, True, True), (8192, 48, 64, False, False)]
     for ci, (K, N, bs, zp, f32) in enumerate(cases):
         t = synth.make_weight(6100 + 10 * M + ci, N, K, bs, with_zp=zp)
@@ -161,7 +163,7 @@ def test_multi_row_products_by_row_group(ctx, M):
 @pytest.mark.parametrize("bs", [16, 256])
 def test_block_sizes_16_and_256(ctx, bs):
     t = synth.make_weight(77 + bs, 200, 1024, bs, with_zp=True)
-    for M in (1, 5, 40):
+    for M in (1, 3, 5, 40):
         x16 = synth.make_x(78 + M, M, 1024)
         y_ref, wmax = oracle_matmul(t, x16)
         w = upload(ctx, t)

@@ -11,7 +11,7 @@
 // 16x128 tile in MFMA operand order, so a wave streams 1 KiB per load.
 // Per 32-k step: 9 VALU ops turn 8 nibbles into 8 exact fp16 (q - zp), one
 // v_mfma_f32_16x16x32_f16 multiplies them with x (A operand; rows 0..15 are
-// the M activation rows, M = 1 broadcasts x to every row), and the block
+// the activation rows, M = 1 broadcasts x to every row), and the block
 // scale is applied to the fp32 MFMA result (bs >= 32), so no weight is ever
 // rounded.  bs = 16 (two scales per 32-k step) folds the scale into the fp16
 // weight instead.
@@ -19,13 +19,22 @@
 
 namespace mnb {
 
-// LDS bytes of one wave's x block when M > 1: 16 rows x 128 k of fp16.
-constexpr int kXBlockBytes = kTileRows * kTileK * 2;
+// LDS bytes of 4 x rows of one super-tile (128 k of fp16).  When M > 1 a
+// wave's x block holds XR of them: 4 XR rows.
+constexpr int kXGroupBytes = 4 * kTileK * 2;
+
+// x row groups of 4 rows a product with M rows loads: M <= 4 XR.
+inline int gemv_rows_xr(int M) { return M <= 4 ? 1 : M <= 8 ? 2 : 4; }
 
 // M1: x has one row, staged once per workgroup in LDS (A operand = x
-// broadcast to all 16 MFMA rows).  !M1: up to 16 rows read from global
-// memory (rows >= M repeat row M-1 and their results are discarded); XR of
-// the 4 groups of 4 rows are loaded (M <= 4 XR), the others are zero.
+// broadcast to all 16 MFMA rows).  !M1: the wave's x block holds 4 XR rows
+// of the super-tile (rows >= M repeat row M-1), and MFMA row m reads block
+// row m * XR / 4: with M <= 4 (XR = 1) the four MFMA rows of lane group g
+// all read x row g, so the lanes of group g hold output row g, one sum per
+// lane; with M <= 8 (XR = 2) group g holds rows 2g and 2g+1, two sums; with
+// M <= 16 (XR = 4) rows 4g..4g+3, four sums.  A smaller block means fewer
+// LDS stores and less LDS per workgroup (more resident workgroups); the
+// duplicated MFMA rows cost nothing, the MFMA issues either way.
 // STW: super-tiles per wave; all of a wave's weight, scale and zero-point
 // loads are issued before any arithmetic.
 // One workgroup computes the 16 outputs of n-tile `nt` (per activation row):
@@ -34,14 +43,20 @@ constexpr int kXBlockBytes = kTileRows * kTileK * 2;
 template <typename ScaleT, bool HAS_ZP, bool M1, int SPS, int STW, int XR = 4>
 __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, unsigned char *smem) {
     constexpr int ZB = SPS <= 2 ? 1 : SPS / 2;
+    static_assert(XR == 1 || XR == 2 || XR == 4, "x row groups: 1, 2 or 4");
+    // !M1: MFMA row m reads x block row m >> RSH; the D values of a lane that
+    // are distinct rows are acc[0], acc[AST], ... (AST = 1 << RSH).  M1
+    // keeps acc[0] only.
+    constexpr int RSH = XR == 4 ? 0 : XR == 2 ? 1 : 2;
+    constexpr int AST = M1 ? 4 : 1 << RSH;
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int W = blockDim.x >> 6;
     float4_t *red = (float4_t *)smem;                              // [W][64]
     // wave-private x region after the reduction slots: M1, the wave's slice
-    // of x (STW*128 halves); !M1, one 16-row x block of a super-tile
-    unsigned char *xw = smem + (size_t)W * 64 * sizeof(float4_t) + (size_t)wave * (M1 ? STW * kTileK * 2 : kXBlockBytes);
+    // of x (STW*128 halves); !M1, the 4 XR-row x block of a super-tile
+    unsigned char *xw = smem + (size_t)W * 64 * sizeof(float4_t) + (size_t)wave * (M1 ? STW * kTileK * 2 : XR * kXGroupBytes);
     _Float16 *xs = (_Float16 *)xw;
     const int r = lane & 15, gg = lane >> 4;
     const int nchunks = (p.ST + STW - 1) / STW;
@@ -62,7 +77,7 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
     // block into MFMA operand order.  (Loading the operand order directly
     // touches 16 rows, 64 bytes each, per load: four times the cache-line
     // requests for the same bytes.)  Rows >= M repeat row M - 1.
-    u32x4_t xrw[M1 ? 1 : STW][4];
+    u32x4_t xrw[M1 ? 1 : STW][XR];
     const _Float16 *xrow[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -80,10 +95,9 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
             if constexpr (!M1) {
                 // clamped into the row; pieces at k >= kx are zeroed in LDS
                 const int k = min((c * STW + t) * kTileK + 8 * (lane & 15), p.kx - 8);
-                // XR groups of 4 rows are loaded (M <= 4 XR); the rest only
-                // feed results that are discarded and stay zero
+                // XR groups of 4 rows are loaded (M <= 4 XR)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) xrw[t][i] = i < XR ? *(const u32x4_t *)(xrow[i] + k) : zero4;
+                for (int i = 0; i < XR; ++i) xrw[t][i] = *(const u32x4_t *)(xrow[i] + k);
             }
             raw[t] = gld_nt(qp + (size_t)st * 64);
             load_scale_row<ScaleT, SPS>(sp + (size_t)st * kTileRows * SPS, sv[t]);
@@ -130,12 +144,13 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
                 // rewritten for the next super-tile right after these reads.
                 const bool kok = kst + 8 * (lane & 15) < p.kx;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < XR; ++i) {
                     const int row = 4 * i + (lane >> 4);
                     *(u32x4_t *)(xw + row * 256 + (((lane & 15) ^ row) & 15) * 16) = kok ? xrw[t][i] : zero4;
                 }
+                const int xq = r >> RSH;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) xa[j] = *(const half8_t *)(xw + r * 256 + (((4 * j + gg) ^ r) & 15) * 16);
+                for (int j = 0; j < 4; ++j) xa[j] = *(const half8_t *)(xw + xq * 256 + (((4 * j + gg) ^ xq) & 15) * 16);
             }
             if constexpr (SPS == 8) {
                 // bs = 16: the lane's 8 k lie in block 2j + gg/2; fold the scale.
@@ -160,12 +175,8 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
                         d = mfma16x16x32(xa[j], unpack_q_minus_zp(raw[t][j], blo, bhi, k6400), d);
                     }
                     const float s = (float)sv[t][i];
-                    acc[0] = fmaf(s, d[0], acc[0]);
-                    if constexpr (!M1) {
-                        acc[1] = fmaf(s, d[1], acc[1]);
-                        acc[2] = fmaf(s, d[2], acc[2]);
-                        acc[3] = fmaf(s, d[3], acc[3]);
-                    }
+#pragma unroll
+                    for (int e = 0; e < 4; e += AST) acc[e] = fmaf(s, d[e], acc[e]);
                 }
             }
         }
@@ -192,19 +203,16 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
         if (wave != 0) return;
         for (int w2 = 1; w2 < W; ++w2) {
             const float4_t o = red[w2 * 64 + lane];
-            acc[0] += o[0];
-            acc[1] += o[1];
-            acc[2] += o[2];
-            acc[3] += o[3];
+#pragma unroll
+            for (int e = 0; e < 4; e += AST) acc[e] += o[e];
         }
     }
 
     // undo the stored scales' factor 2^fold_exp (exact)
-    acc[0] *= p.unfold;
-    acc[1] *= p.unfold;
-    acc[2] *= p.unfold;
-    acc[3] *= p.unfold;
-    // D layout of the 16x16 MFMA result: lane (gg*16 + r) holds rows 4*gg+i, column r.
+#pragma unroll
+    for (int e = 0; e < 4; e += AST) acc[e] *= p.unfold;
+    // D layout of the 16x16 MFMA result: lane (gg*16 + r) holds MFMA rows
+    // 4*gg+i, column r; MFMA row m is x row m >> RSH.
     const int n = nt * kTileRows + r;
     if (n >= p.N) return;
     const bool accum = p.accumulate != 0;
@@ -215,8 +223,8 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int mm = 4 * gg + i;
+        for (int i = 0; i < 4; i += AST) {
+            const int mm = (4 * gg + i) >> RSH;
             if (mm < p.M) {
                 const size_t idx = (size_t)mm * p.N + n;
                 if (p.y_f16) store_y<true>(p.y, idx, acc[i], accum);
@@ -253,10 +261,11 @@ template <typename ScaleT, bool HAS_ZP, bool M1, int SPS>
 static hipError_t gemv_stw(const GemvLaunch &L, const GemvParams &p, hipStream_t s) {
     if constexpr (!M1) {
         if (L.stw != kGemvRowsSTW) return hipErrorInvalidValue;
-        // x row groups to load: one per 4 rows of M
-        if (p.M <= 4)
+        // x row groups to load: one per 4 rows of M (the LDS size follows)
+        const int xr = gemv_rows_xr(p.M);
+        if (xr == 1)
             hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, false, SPS, kGemvRowsSTW, 1>), L.grid, L.block, L.lds, s, p);
-        else if (p.M <= 8)
+        else if (xr == 2)
             hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, false, SPS, kGemvRowsSTW, 2>), L.grid, L.block, L.lds, s, p);
         else
             hipLaunchKernelGGL((gemv_kernel<ScaleT, HAS_ZP, false, SPS, kGemvRowsSTW, 4>), L.grid, L.block, L.lds, s, p);
@@ -289,7 +298,7 @@ static hipError_t gemv_zp(const WeightGeom &g, const GemvLaunch &L, const GemvPa
 
 // Super-tiles per wave: 4 (4 KiB of weights in flight per wave), or 2 when
 // the grid would otherwise have fewer than 8 waves per CU.  M > 1 always
-// takes 2 (kGemvRowsSTW): each super-tile also holds 16 registers of x rows.
+// takes 2 (kGemvRowsSTW): each super-tile also holds 4 XR registers of x rows.
 // K above 16 waves x 4 x 128 = 8192 (12 waves x 2 x 128 = 3072 when M > 1)
 // loops over further chunks per wave.
 static int gemv_stw_for(const WeightGeom &g, int cu_count, bool m1) {
@@ -323,17 +332,17 @@ hipError_t launch_gemv(const mnb_weight *w, const MatmulArgs &a, int32_t cu_coun
     waves = min(waves, m1 ? kGemvMaxWaves : kGemvMaxWavesRows);
     L.grid = dim3(g.NT);
     L.block = dim3(64 * waves);
-    L.lds = (size_t)waves * 64 * sizeof(float4_t) + (size_t)waves * (m1 ? L.stw * kTileK * 2 : kXBlockBytes);
+    L.lds = (size_t)waves * 64 * sizeof(float4_t) + (size_t)waves * (m1 ? L.stw * kTileK * 2 : gemv_rows_xr(a.M) * kXGroupBytes);
     return g.scale_f32 ? gemv_zp<float>(g, L, p, m1, stream) : gemv_zp<_Float16>(g, L, p, m1, stream);
 }
 
 hipError_t launch_gemv_group(const GemvGroupPlan &g, hipStream_t stream) {
     dim3 grid(g.total_wgs), block(64 * g.waves);
-    const size_t lds = (size_t)g.waves * 64 * sizeof(float4_t) + (size_t)g.waves * (g.m1 ? 4 * kTileK * 2 : kXBlockBytes);
+    // M > 1: x row groups to load, from the largest M of the items (the LDS size follows)
+    const int xr = g.m1 ? 4 : gemv_rows_xr(g.max_m);
+    const size_t lds = (size_t)g.waves * 64 * sizeof(float4_t) + (size_t)g.waves * (g.m1 ? 4 * kTileK * 2 : xr * kXGroupBytes);
     const GroupItem *it = (const GroupItem *)g.items;
     const uint16_t *wi = (const uint16_t *)g.wg_item;
-    // M > 1: x row groups to load, from the largest M of the items
-    const int xr = g.m1 || g.max_m > 8 ? 4 : g.max_m > 4 ? 2 : 1;
 #define MNB_GROUP_XR(ST_, ZP_, M1_, SPS_, XR_) \
     hipLaunchKernelGGL((gemv_group_kernel<ST_, ZP_, M1_, SPS_, M1_ ? 4 : kGemvRowsSTW, XR_>), grid, block, lds, stream, it, wi)
 #define MNB_GROUP_LAUNCH(ST_, ZP_, M1_, SPS_)                                    \
