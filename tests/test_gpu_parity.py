@@ -156,7 +156,13 @@ def test_multi_row_products_by_row_group(ctx, M):
         w = upload(ctx, t, as_f32_scales=f32)
         label = "rows M=%d K=%d N=%d bs=%d zp=%d f32=%d" % (M, K, N, bs, zp, f32)
         say(label)
-        assert_parity(w.matmul(x16, out_dtype=np.float16), y_ref, x16, t, wmax, True, label)
+        y32 = w.matmul(x16)
+        assert_parity(y32, y_ref, x16, t, wmax, False, label)
+        y16 = w.matmul(x16, out_dtype=np.float16)
+        assert np.array_equal(y16.view(np.uint16), y32.astype(np.float16).view(np.uint16)), label
+        y0 = np.random.default_rng(M + ci).standard_normal((M, N)).astype(np.float32)
+        acc = w.matmul(x16, y=y0.copy(), accumulate=True)
+        assert np.array_equal(acc.view(np.uint32), (y0 + y32).view(np.uint32)), label
         w.close()
 
 
