@@ -78,9 +78,9 @@ __device__ __forceinline__ void gemv_tile(const GemvParams &p, const int nt, uns
     // touches 16 rows, 64 bytes each, per load: four times the cache-line
     // requests for the same bytes.)  Rows >= M repeat row M - 1.
     u32x4_t xrw[M1 ? 1 : STW][XR];
-    const _Float16 *xrow[4];
+    const _Float16 *xrow[XR];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < XR; ++i) {
         const int row = 4 * i + (lane >> 4);
         xrow[i] = p.x + (size_t)(row < p.M ? row : p.M - 1) * p.ldx;
     }
