@@ -676,13 +676,24 @@ def main():
         wall512s * 1e6, gpu512s * 1e6, tflops512s, kernel_tflops512s))
     del la512
     sweep, sweep_seq = {}, {}
+    # both fractions per M (M = 128 sits near the ridge of the two rooflines)
+    frac, frac_seq = {}, {}
+
+    def fractions(M, fl, w_m):
+        nb = sum(t.algorithmic_bytes(M) for t in host)
+        return {"tflops": round(fl / w_m / 1e12, 2), "frac_fp16_peak": round(fl / w_m / 1e12 / FP16_PEAK_TFLOPS, 4),
+                "gbs": round(nb / w_m / 1e9, 1), "frac_hbm_peak": round(nb / w_m / 1e9 / HBM_PEAK_GBS, 4),
+                "flop_per_byte": round(fl / nb, 1)}
+
     if not args.no_sweep:
         for M in (16, 128, 2048):
             _, fl, w_m, _ = prefill(M, group=True)
             sweep[str(M)] = round(fl / w_m / 1e12, 2)
+            frac[str(M)] = fractions(M, fl, w_m)
             torch.cuda.empty_cache()
             _, fl, w_m, _ = prefill(M)
             sweep_seq[str(M)] = round(fl / w_m / 1e12, 2)
+            frac_seq[str(M)] = fractions(M, fl, w_m)
             torch.cuda.empty_cache()
             log("prefill M=%d: %.1f TFLOP/s as one group launch, %.1f as 129 launches" % (
                 M, sweep[str(M)], sweep_seq[str(M)]))
@@ -765,7 +776,7 @@ def main():
                                       "traffic_unit": "HBM bytes per step (one launch)",
                                       "traffic_source": "profiles/gemm_sk_phi3_prefill_m512_group.md "
                                                         "(rocprofv3 FETCH_SIZE + WRITE_SIZE)"},
-                         "sweep_tflops": sweep},
+                         "sweep_tflops": sweep, "sweep_fractions": frac},
         "prefill_m512_sequential": {
                          "tflops": round(tflops512s, 2), "ms_per_step": round(wall512s * 1e3, 4),
                          "frac_fp16_peak": round(tflops512s / FP16_PEAK_TFLOPS, 4),
@@ -780,7 +791,7 @@ def main():
                                       "traffic_unit": "HBM bytes per step (129 launches)",
                                       "traffic_source": "profiles/gemm_sk_phi3_prefill_m512.md "
                                                         "(rocprofv3 FETCH_SIZE + WRITE_SIZE)"},
-                         "sweep_tflops": sweep_seq},
+                         "sweep_tflops": sweep_seq, "sweep_fractions": frac_seq},
         "small_batch_decode": dict(small_batch, note="the 129 projections with M rows each recorded as one group "
                                                      "(mnb::gemv_stream_kernel with M activation rows per job)"),
         "device_copy_gbs": round(copy_gbs, 1),
