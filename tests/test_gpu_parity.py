@@ -949,6 +949,35 @@ def test_single_products_with_a_k_tail_not_a_multiple_of_8(ctx, K):
             w.close()
 
 
+@pytest.mark.parametrize("N,K,bs,zp", [(1, 32, 32, False), (1, 8, 16, True), (17, 40, 32, True), (5, 136, 64, False),
+                                        (33, 128, 128, True), (2, 264, 256, False)])
+def test_tiny_shapes_on_every_path(ctx, N, K, bs, zp):
+    """The smallest shapes: one output column (N = 1, a 16-row n-tile with 15
+    padding rows, and 128- or 256-column GEMM tiles of one column), K below
+    one 128-k super-tile or a block (K = 8 with bs 16, K = 40 with bs 32), a
+    block larger than K; M from 1 to 130, so each single-product path runs
+    (GEMV with one, two and four x row groups, the K-sliced kernel, the
+    GEMM).  fp32 y against the oracle, fp16 y as the rounded fp32 result,
+    y += bitwise."""
+    t = synth.make_weight(8700 + N + K + bs, N, K, bs, with_zp=zp)
+    w = upload(ctx, t)
+    try:
+        for M in (1, 2, 3, 5, 8, 12, 16, 17, 40, 130):
+            x16 = synth.make_x(8800 + M + K, M, K)
+            y_ref, wmax = oracle_matmul(t, x16)
+            label = "tiny N=%d K=%d bs=%d zp=%d M=%d plan=%s" % (N, K, bs, zp, M, w.plan(M).as_tuple())
+            say(label)
+            y32 = w.matmul(x16)
+            assert_parity(y32, y_ref, x16, t, wmax, False, label)
+            y16 = w.matmul(x16, out_dtype=np.float16)
+            assert np.array_equal(y16.view(np.uint16), y32.astype(np.float16).view(np.uint16)), label
+            y0 = np.random.default_rng(M + N).standard_normal(y32.shape).astype(np.float32)
+            acc = w.matmul(x16, y=y0.copy(), accumulate=True)
+            assert np.array_equal(acc.view(np.uint32), (y0 + y32).view(np.uint32)), label
+    finally:
+        w.close()
+
+
 @pytest.mark.parametrize("case", [(500, 3000, 32001, 32, True, False, np.float32, False),
                                   (2048, 1024, 16384, 64, False, False, np.float16, True),
                                   (512, 3072, 32064, 128, False, True, np.float16, False)],
