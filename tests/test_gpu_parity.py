@@ -955,10 +955,11 @@ def test_tiny_shapes_on_every_path(ctx, N, K, bs, zp):
     """The smallest shapes: one output column (N = 1, a 16-row n-tile with 15
     padding rows, and 128- or 256-column GEMM tiles of one column), K below
     one 128-k super-tile or a block (K = 8 with bs 16, K = 40 with bs 32), a
-    block larger than K; M from 1 to 130, so each single-product path runs
-    (GEMV with one, two and four x row groups, the K-sliced kernel, the
-    GEMM).  fp32 y against the oracle, fp16 y as the rounded fp32 result,
-    y += bitwise."""
+    block larger than K; M from 1 to 130, so each single-product path the
+    planners pick at these sizes runs (the GEMV with one, two and four x
+    row groups, and the K-sliced kernel; groups of such products run the
+    GEMM, in the test below).  fp32 y against the oracle, fp16 y as the
+    rounded fp32 result, y += bitwise."""
     t = synth.make_weight(8700 + N + K + bs, N, K, bs, with_zp=zp)
     w = upload(ctx, t)
     try:
@@ -975,6 +976,19 @@ def test_tiny_shapes_on_every_path(ctx, N, K, bs, zp):
             acc = w.matmul(x16, y=y0.copy(), accumulate=True)
             assert np.array_equal(acc.view(np.uint32), (y0 + y32).view(np.uint32)), label
     finally:
+        w.close()
+
+
+@pytest.mark.parametrize("bs,Ks", [(16, (8, 40, 136)), (32, (32, 40, 264))])
+def test_tiny_shapes_in_prefill_groups(ctx, bs, Ks):
+    """The same small shapes recorded as groups with M > 16, which always
+    run the GEMM: one output column (N = 1: one n-tile under a 256- or
+    512-column tile), K below a super-tile or a block, fp16 and fp32 y, y +=;
+    every item against the oracle and its own single launch, replays
+    bitwise identical."""
+    specs = [(17, Ks[0], 1, np.float16, False), (130, Ks[1], 17, np.float32, False),
+             (40, Ks[2], 5, np.float16, True), (33, Ks[0], 33, np.float32, True)]
+    for w, _, _ in _check_prefill_group(ctx, specs, 9100 + bs, bs=bs):
         w.close()
 
 
