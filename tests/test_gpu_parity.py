@@ -979,16 +979,20 @@ def test_tiny_shapes_on_every_path(ctx, N, K, bs, zp):
         w.close()
 
 
+@pytest.mark.parametrize("ms", [(1, 1, 1, 1), (2, 3, 4, 2), (6, 5, 8, 6), (17, 130, 40, 33)],
+                         ids=["m1-stream", "small-batch-stream", "gemv-group", "gemm"])
 @pytest.mark.parametrize("bs,Ks", [(16, (8, 40, 136)), (32, (32, 40, 264))])
-def test_tiny_shapes_in_prefill_groups(ctx, bs, Ks):
-    """The same small shapes recorded as groups with M > 16, which always
-    run the GEMM: one output column (N = 1: one n-tile under a 256- or
-    512-column tile), K below a super-tile or a block, fp16 and fp32 y, y +=;
-    every item against the oracle and its own single launch, replays
-    bitwise identical."""
-    specs = [(17, Ks[0], 1, np.float16, False), (130, Ks[1], 17, np.float32, False),
-             (40, Ks[2], 5, np.float16, True), (33, Ks[0], 33, np.float32, True)]
-    for w, _, _ in _check_prefill_group(ctx, specs, 9100 + bs, bs=bs):
+def test_tiny_shapes_in_groups(ctx, bs, Ks, ms):
+    """The same small shapes recorded as groups of each M class: M = 1 and
+    2 <= M <= 4 (the streaming kernel: units of one super-tile, so a job
+    re-loads it for its missing tiles), 4 < M <= 8 with few tiles (the GEMV
+    over every item's n-tiles) and M > 16 (the GEMM: one n-tile under a
+    256- or 512-column tile); N = 1, K below a super-tile or a block, fp16
+    and fp32 y, y +=; every item against the oracle and its own single
+    launch, replays bitwise identical."""
+    specs = [(ms[0], Ks[0], 1, np.float16, False), (ms[1], Ks[1], 17, np.float32, False),
+             (ms[2], Ks[2], 5, np.float16, True), (ms[3], Ks[0], 33, np.float32, True)]
+    for w, _, _ in _check_prefill_group(ctx, specs, 9100 + bs + sum(ms), bs=bs):
         w.close()
 
 
