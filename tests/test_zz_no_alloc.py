@@ -57,8 +57,8 @@ def _both(ctx, w, x, ydt, acc=False):
 # (M, K, N, zero points, x dtype, unaligned x, y dtype, y +=): split GEMM
 # tiles (stream-K partials in the scratch array), the K-sliced kernel (also
 # with 16-row blocks at M <= 16), staged x (fp32, K % 8 != 0, a misaligned
-# pointer), the M <= 16 kernels; each case is followed by a smaller one of
-# the same kind.
+# pointer), the M <= 16 kernels (the GEMV with one, two and four x row
+# groups); each case is followed by a smaller one of the same kind.
 CASES = [
     ((200, 8192, 9001, False, "f16", False, "f16", False), (150, 8192, 9001, False, "f16", False, "f16", False)),
     ((200, 3072, 1000, False, "f16", False, "f16", False), (130, 3072, 1000, False, "f16", False, "f16", False)),
@@ -68,6 +68,7 @@ CASES = [
     ((1, 3072, 9216, False, "f32", False, "f16", False), (1, 3072, 3072, False, "f16", False, "f32", True)),
     ((16, 1003, 500, True, "f32", False, "f16", False), (5, 1003, 500, True, "f16", True, "f16", False)),
     ((16, 3001, 16000, True, "f32", False, "f16", False), (12, 3001, 16000, True, "f16", True, "f32", True)),
+    ((8, 2000, 3000, False, "f32", False, "f16", False), (3, 2000, 3000, False, "f16", True, "f32", True)),
 ]
 
 
