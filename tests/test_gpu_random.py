@@ -1,0 +1,66 @@
+"""Seeded random single products through every path the planners choose.
+
+Each case draws M from one of the size classes (1; 2..8; 9..16; 17..64;
+65..600), K from 8 to 6000 (mostly multiples of 8, else x is staged), N
+from 1 to 40000, a block size from 16 to 256 and zero points or not, and
+checks mnb_matmul against the oracle on up to 256 sampled output columns:
+fp32 y within the parity bound, fp16 y the rounded fp32 y, and y += equal
+to y0 + y bit for bit.  The planners' choice (GEMV, K-sliced kernel, GEMM
+in stream-K or tile-list order) is printed with each case."""
+import numpy as np
+import pytest
+
+import mnb_hip
+from mnb_hip import synth
+import mnb_oracle as orc
+from parity_util import assert_parity, oracle_matmul, say, upload
+
+pytestmark = pytest.mark.gpu
+
+CASES_PER_SEED = 16
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    orc.build()
+    c = mnb_hip.Context(0)
+    yield c
+    c.close()
+
+
+def _draw(rng):
+    cls = int(rng.integers(0, 5))
+    M = [1, int(rng.integers(2, 9)), int(rng.integers(9, 17)), int(rng.integers(17, 65)), int(rng.integers(65, 601))][cls]
+    bs = int(rng.choice([16, 32, 64, 128, 256]))
+    K = int(rng.integers(8, 6001))
+    if rng.random() < 0.7:
+        K -= K % 8
+    K = max(K, 8)
+    N = [int(rng.integers(1, 64)), int(rng.integers(64, 4096)), int(rng.integers(4096, 40001))][int(rng.integers(0, 3))]
+    zp = bool(rng.random() < 0.5)
+    return M, K, N, bs, zp
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_random_single_products(ctx, seed):
+    rng = np.random.default_rng(70000 + seed)
+    for case in range(CASES_PER_SEED):
+        M, K, N, bs, zp = _draw(rng)
+        t = synth.make_weight(71000 + 100 * seed + case, N, K, bs, with_zp=zp)
+        w = upload(ctx, t)
+        try:
+            label = "random seed=%d case=%d M=%d K=%d N=%d bs=%d zp=%d plan=%s" % (
+                seed, case, M, K, N, bs, zp, w.plan(M).as_tuple())
+            say(label)
+            x16 = synth.make_x(72000 + 100 * seed + case, M, K)
+            rows = np.sort(rng.choice(N, min(N, 256), replace=False))
+            y_ref, wmax = oracle_matmul(t, x16, rows)
+            y32 = w.matmul(x16).reshape(M, N)
+            assert_parity(y32[:, rows], y_ref.reshape(M, -1), x16, t, wmax, False, label)
+            y16 = w.matmul(x16, out_dtype=np.float16).reshape(M, N)
+            assert np.array_equal(y16.view(np.uint16), y32.astype(np.float16).view(np.uint16)), label
+            y0 = rng.standard_normal((M, N)).astype(np.float32)
+            acc = w.matmul(x16, y=y0.copy(), accumulate=True).reshape(M, N)
+            assert np.array_equal(acc.view(np.uint32), (y0 + y32).view(np.uint32)), label
+        finally:
+            w.close()
