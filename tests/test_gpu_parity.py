@@ -662,6 +662,28 @@ def test_random_prefill_groups(ctx, seed):
         w.close()
 
 
+@pytest.mark.parametrize("cls", ["m1", "rows2to4", "rows5to16"])
+@pytest.mark.parametrize("seed", [0, 1])
+def test_random_small_groups(ctx, cls, seed):
+    """Random groups of M <= 16 products: all M = 1 (the streaming kernel),
+    2 <= M <= 4 (the streaming kernel with the group's largest M rows of x
+    per job) or 5 <= M <= 16 (the GEMV over every item's n-tiles, or 32-row
+    GEMM tiles when there are many); 3 to 10 items, K a multiple of 8 up to
+    4096, N up to 12000, one block size per group, fp16 or fp32 y, y += or
+    not; every item against the oracle and its own single launch."""
+    ci = {"m1": 0, "rows2to4": 1, "rows5to16": 2}[cls]
+    rng = np.random.default_rng(7300 + 10 * seed + ci)
+    lo, hi = [(1, 1), (2, 4), (5, 16)][ci]
+    bs = int(rng.choice([16, 32, 64, 128, 256]))
+    specs = []
+    for _ in range(int(rng.integers(3, 11))):
+        M, K, N = int(rng.integers(lo, hi + 1)), 8 * int(rng.integers(1, 513)), int(rng.integers(1, 12001))
+        specs.append((M, K, N, [np.float16, np.float32][int(rng.integers(0, 2))], bool(rng.random() < 0.3)))
+    say("random small group", cls, seed, "bs", bs, [sp[:3] for sp in specs])
+    for w, _, _ in _check_prefill_group(ctx, specs, 7400 + 10 * seed + ci, bs=bs):
+        w.close()
+
+
 @pytest.mark.parametrize("ms", [(6, 3), (13, 2, 8), (8, 5)])
 def test_small_groups_of_multi_row_products(ctx, ms):
     """Groups with 4 < M <= 16 (largest M of the group) and few 32 x 512
