@@ -1,7 +1,7 @@
 """Seeded random single products through every path the planners choose.
 
 Each case draws M from one of the size classes (1; 2..8; 9..16; 17..64;
-65..600), K from 8 to 6000 (mostly multiples of 8, else x is staged), N
+65..600; and 601..3000 in a test of its own), K from 8 to 6000 (mostly multiples of 8, else x is staged), N
 from 1 to 40000, a block size from 16 to 256 and zero points or not, and
 checks mnb_matmul against the oracle on up to 256 sampled output columns:
 fp32 y within the parity bound, fp16 y the rounded fp32 y, and y += equal
@@ -62,5 +62,28 @@ def test_random_single_products(ctx, seed):
             y0 = rng.standard_normal((M, N)).astype(np.float32)
             acc = w.matmul(x16, y=y0.copy(), accumulate=True).reshape(M, N)
             assert np.array_equal(acc.view(np.uint32), (y0 + y32).view(np.uint32)), label
+        finally:
+            w.close()
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_random_large_single_products(ctx, seed):
+    rng = np.random.default_rng(73000 + seed)
+    for case in range(4):
+        M, K, N = int(rng.integers(601, 3001)), int(rng.integers(8, 6001)), int(rng.integers(1, 20001))
+        bs, zp = int(rng.choice([16, 32, 64, 128, 256])), bool(rng.random() < 0.5)
+        t = synth.make_weight(74000 + 100 * seed + case, N, K, bs, with_zp=zp)
+        w = upload(ctx, t)
+        try:
+            label = "random large seed=%d case=%d M=%d K=%d N=%d bs=%d zp=%d plan=%s" % (
+                seed, case, M, K, N, bs, zp, w.plan(M).as_tuple())
+            say(label)
+            x16 = synth.make_x(75000 + 100 * seed + case, M, K)
+            rows = np.sort(rng.choice(N, min(N, 128), replace=False))
+            y_ref, wmax = oracle_matmul(t, x16, rows)
+            y32 = w.matmul(x16).reshape(M, N)
+            assert_parity(y32[:, rows], y_ref.reshape(M, -1), x16, t, wmax, False, label)
+            y16 = w.matmul(x16, out_dtype=np.float16).reshape(M, N)
+            assert np.array_equal(y16.view(np.uint16), y32.astype(np.float16).view(np.uint16)), label
         finally:
             w.close()
