@@ -39,12 +39,16 @@ def zp_blocks(t: synth.QuantTensor) -> np.ndarray:
     return nib[:, :kb].reshape(-1)
 
 
-def oracle_inputs(t: synth.QuantTensor, rows=None):
-    """Reference-form tensors: fp32 scales (loader widening), flat zero points
-    (runtime layout; 0x88 when absent), optionally restricted to `rows`."""
+def oracle_inputs(t: synth.QuantTensor, rows=None, scales=None):
+    """Reference-form tensors: fp32 scales (loader widening, or `scales` [N*kb]
+    fp32 as uploaded), flat zero points (runtime layout; 0x88 when absent),
+    optionally restricted to `rows`."""
     kb, bs = t.kb, t.bs
     q = t.q.reshape(t.N, kb * bs // 2)
-    s = orc.fp16_bits_to_fp32(t.scales_f16.view(np.uint16)).reshape(t.N, kb)
+    if scales is not None:
+        s = np.asarray(scales, np.float32).reshape(t.N, kb)
+    else:
+        s = orc.fp16_bits_to_fp32(t.scales_f16.view(np.uint16)).reshape(t.N, kb)
     if t.zp_row_padded is not None:
         zrp = t.zp_row_padded
     else:
@@ -56,11 +60,12 @@ def oracle_inputs(t: synth.QuantTensor, rows=None):
     return q.reshape(-1), s.reshape(-1), z, n
 
 
-def oracle_matmul(t: synth.QuantTensor, x16: np.ndarray, rows=None, want_wmax=True):
+def oracle_matmul(t: synth.QuantTensor, x16: np.ndarray, rows=None, want_wmax=True, scales=None):
     """The oracle's y = x W^T (fp32) for output columns `rows` (all when None),
     and max|w| when asked for and the dequantized weight is small enough to
-    form (else None)."""
-    q, s, z, n = oracle_inputs(t, rows)
+    form (else None).  `scales`: fp32 scales [N*kb] uploaded instead of the
+    tensor's fp16 ones."""
+    q, s, z, n = oracle_inputs(t, rows, scales)
     kpad = t.kb * t.bs
     M = x16.shape[0]
     x = np.zeros((M, kpad), np.float32)
@@ -72,10 +77,11 @@ def oracle_matmul(t: synth.QuantTensor, x16: np.ndarray, rows=None, want_wmax=Tr
     return y, wmax
 
 
-def max_abs_w(t: synth.QuantTensor) -> float:
-    """An upper bound of max|w|: max over blocks of |scale| times the largest
-    |q - zp| the zero-point layout allows (15 with zero points, 8 without)."""
-    s = t.scales_f16.astype(np.float32).reshape(t.N, t.kb)
+def max_abs_w(t: synth.QuantTensor, scales=None) -> float:
+    """An upper bound of max|w|: max over blocks of |scale| (the tensor's fp16
+    scales, or `scales`) times the largest |q - zp| the zero-point layout
+    allows (15 with zero points, 8 without)."""
+    s = t.scales_f16.astype(np.float32) if scales is None else np.asarray(scales, np.float32)
     return float(np.max(np.abs(s)) * 15.0) if t.zp_row_padded is not None else float(np.max(np.abs(s)) * 8.0)
 
 

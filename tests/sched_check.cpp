@@ -112,11 +112,37 @@ static int check_closed() {
     return 0;
 }
 
+// The single-product planner's grids against the workspace they need: for
+// lines "cu_count M NT ST scale_f32 sps", sk_grid and sk_single_plan never
+// pick more than sk_max_grid(cu_count) <= kSkMaxGrid workgroups, nor more
+// workgroups than iterations, so the partial tiles of any plan fit
+// sk_workspace_bytes(kSkMaxGrid) -- the size of the context's workspace on a
+// device of at least kSkMaxGrid CUs and of mnb_matmul_noalloc's fixed array.
+static int check_grid() {
+    int cu, M, NT, ST, f32, sps, cases = 0;
+    while (scanf("%d %d %d %d %d %d", &cu, &M, &NT, &ST, &f32, &sps) == 6) {
+        const int cap = sk_max_grid(cu);
+        if (cap < 1 || cap > kSkMaxGrid || cap > cu) return fail("max grid", cu, cap);
+        const int T = sk_tiles(M, NT);
+        const int G = sk_grid(T, ST, cu);
+        if (G < 1 || G > cap || (int64_t)G > (int64_t)T * ST) return fail("sk_grid", cu * 100000L + T, G);
+        if (sk_workspace_bytes(G) > sk_workspace_bytes(kSkMaxGrid)) return fail("workspace", G, kSkMaxGrid);
+        const SinglePlan p = sk_single_plan(M, NT, ST, f32, sps, cu);
+        if (p.G < 1 || p.G > cap) return fail("single plan grid", cu, p.G);
+        if (p.closed ? (p.ntw != kGemmWideNTW || !sk_wide_supported(f32, sps)) : (p.ntw != kGemmNTW || p.G != G))
+            return fail("single plan shape", p.ntw, p.G);
+        ++cases;
+    }
+    printf("ok grid cases=%d\n", cases);
+    return 0;
+}
+
 int main() {
     char first[32] = {0};
     if (scanf("%31s", first) != 1) return fail("input", 0, 0);
     if (strcmp(first, "stream") == 0) return check_stream();
     if (strcmp(first, "closed") == 0) return check_closed();
+    if (strcmp(first, "grid") == 0) return check_grid();
     const int G = atoi(first);
     if (G < 1) return fail("input", G, 0);
     std::vector<SkItem> items;

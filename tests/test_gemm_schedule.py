@@ -151,3 +151,23 @@ def test_closed_form_equals_the_table_of_a_single_item(checker):
                                       int(rng.integers(1, 70))))
     r = subprocess.run([checker], input="closed\n" + "\n".join(lines) + "\n", capture_output=True, text=True)
     assert r.returncode == 0 and r.stdout.startswith("ok closed cases=%d" % len(lines)), r.stdout
+
+
+def test_planner_grids_fit_the_workspace(checker):
+    """sk_grid and sk_single_plan (the single-product GEMM planner) never pick
+    more workgroups than sk_max_grid(cu_count) <= 256 nor more than the
+    launch's iterations, for devices of 1 to 1024 CUs, so the partial tiles of
+    every plan fit the workspace of the largest grid -- the context's
+    workspace and the fixed scratch array of mnb_matmul_noalloc
+    (mnb_noalloc.hip), whose size check uses the same plan."""
+    rng = np.random.default_rng(17)
+    lines = []
+    for cu in (1, 7, 32, 80, 104, 200, 240, 255, 256, 257, 304, 512, 1024):
+        for M, NT, ST in [(512, 576, 24), (512, 192, 24), (512, 1024, 24), (512, 192, 64), (512, 2004, 24),
+                          (17, 1, 1), (2048, 9496, 7), (140000, 192, 64)]:
+            lines.append("%d %d %d %d 0 4" % (cu, M, NT, ST))
+        for _ in range(40):
+            lines.append("%d %d %d %d %d %d" % (cu, rng.integers(17, 5000), rng.integers(1, 3000), rng.integers(1, 120),
+                                                rng.integers(0, 2), 2 ** rng.integers(0, 4)))
+    r = subprocess.run([checker], input="grid\n" + "\n".join(lines) + "\n", capture_output=True, text=True)
+    assert r.returncode == 0 and r.stdout.startswith("ok grid cases=%d" % len(lines)), r.stdout

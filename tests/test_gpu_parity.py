@@ -9,6 +9,7 @@ Bars (stated per test):
   hold bit-for-bit (power-of-two scaling, row independence of the skinny
   kernel, run-to-run determinism of the GEMM and the K-sliced kernel).
 """
+import ctypes
 import os
 import subprocess
 
@@ -340,7 +341,13 @@ def test_gemm_split_tiles_tails_and_outputs(ctx, M, K, N):
     (13, 2500, 16000, 64, True, False, (16, 64)),
     (14, 1500, 30000, 16, False, False, (16, 64)),
     (9, 3001, 20000, 128, True, False, (16, 64)),
-    (11, 3000, 16001, 32, False, True, (16, 64))],
+    (11, 3000, 16001, 32, False, True, (16, 64)),
+    # fp32 scales with zero points (the tied head's quantizer and subnormal
+    # fp16 scales give such weights) at bs 16, 32 and 64
+    (40, 1024, 600, 16, True, True, (32, 16)),
+    (33, 1000, 300, 32, True, True, (32, 16)),
+    (60, 3000, 2000, 64, True, True, (32, 16)),
+    (48, 1536, 4000, 16, True, True, (32, 32))],
     ids=lambda c: "M%d-K%d-N%d-bs%d%s%s" % (c[0], c[1], c[2], c[3], "-zp" if c[4] else "", "-f32s" if c[5] else ""))
 def test_single_products_k_sliced(ctx, case):
     """Single products where the GEMM would have few tiles run on the
@@ -355,27 +362,23 @@ def test_single_products_k_sliced(ctx, case):
     import torch
     M, K, N, bs, zp, f32s, block = case
     t = synth.make_weight(9100 + M + N, N, K, bs, with_zp=zp)
+    s = None
     if f32s:    # scales that fp16 cannot hold: the device keeps fp32 scales
         s = t.scales_f16.astype(np.float32) * np.float32(1.0 + 2.0 ** -14)
-        w = mnb_hip.Weight(ctx, N, K, bs, t.q, s)
+        if zp:
+            w = mnb_hip.Weight(ctx, N, K, bs, t.q, s, t.zp_row_padded, mnb_hip.MNB_ZP_ROW_PADDED)
+        else:
+            w = mnb_hip.Weight(ctx, N, K, bs, t.q, s)
     else:
         w = upload(ctx, t)
     try:
         p = w.plan(M)
-        if f32s:
+        if f32s and not zp:
             assert p.kernel == KSLICE, p.as_tuple()
         else:
             assert p.as_tuple() == (KSLICE, NO_ORDER) + block, p.as_tuple()
         x16 = synth.make_x(9200 + M, M, K)
-        if f32s:
-            kb = t.kb
-            z = synth.zp_row_padded_to_flat(np.full((N, (kb + 1) // 2), 0x88, np.uint8), N, kb)
-            xp = np.zeros((M, kb * bs), np.float32)
-            xp[:, :K] = x16.astype(np.float32)
-            y_ref = orc.matmul(t.q, s, z, N, kb * bs, bs, xp, threads=THREADS)
-            wmax = float(np.abs(s).max()) * 8.0
-        else:
-            y_ref, wmax = oracle_matmul(t, x16)
+        y_ref, wmax = oracle_matmul(t, x16, scales=s)
         label = "k-sliced M=%d K=%d N=%d bs=%d" % (M, K, N, bs)
         y32 = w.matmul(x16)
         assert_parity(y32, y_ref, x16, t, wmax, False, label)
@@ -490,6 +493,14 @@ def test_error_paths(ctx):
     finally:
         del os.environ["MNB_FAULT_INJECT"]
     w = mnb_hip.Weight(ctx, 64, 256, 32, t.q, t.scales_f16)     # recovers after the injected failure
+    # a weight of another context: the plan query refuses it like the product does
+    ctx2 = mnb_hip.Context(0)
+    try:
+        info = mnb_hip.PlanInfo()
+        rc = mnb_hip.load().mnb_matmul_plan(ctx2.handle, w.handle, 40, ctypes.byref(info))
+        assert rc == mnb_hip.MNB_ERR_INVALID_ARGUMENT and "another context" in mnb_hip.last_error(), rc
+    finally:
+        ctx2.close()
     w.close()
 
 
@@ -715,6 +726,18 @@ def test_small_batch_groups_on_the_streaming_kernel(ctx, bs, ms):
     specs = [(M, K, N, ydt, False) for M, (K, N, ydt) in zip(ms, shapes)]
     specs += [(ms[0], 896, 1152, np.float16, True), (ms[-1], 2048, 300, np.float32, True)]
     for w, _, _ in _check_prefill_group(ctx, specs, 2900 + bs + sum(ms), bs=bs, plan=(STREAM, NO_ORDER, rows, 16)):
+        w.close()
+
+
+@pytest.mark.parametrize("ms", [(1, 1), (3, 2)])
+def test_group_with_an_item_of_more_than_65536_n_tiles(ctx, ms):
+    """The streaming kernel codes an item's n-tile in 16 bits, so a group of
+    M <= 4 products with an item of N > 1048576 (65537 n-tiles) runs on the
+    GEMV group kernel instead of failing: each item against the oracle on
+    sampled columns and against its own single
+    launch."""
+    specs = [(ms[0], 64, 1048592, np.float32, False), (ms[1], 1000, 300, np.float16, False)]
+    for w, _, _ in _check_prefill_group(ctx, specs, 9700 + sum(ms), plan=(GEMV_GROUP, NO_ORDER, 0, 16)):
         w.close()
 
 

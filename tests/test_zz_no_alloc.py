@@ -61,6 +61,9 @@ def _both(ctx, w, x, ydt, acc=False):
 # groups); each case is followed by a smaller one of the same kind.
 CASES = [
     ((200, 8192, 9001, False, "f16", False, "f16", False), (150, 8192, 9001, False, "f16", False, "f16", False)),
+    # both regions of the array in one call: staged x (fp32, then a misaligned
+    # fp16 pointer) with split stream-K tiles
+    ((200, 8192, 9001, True, "f32", False, "f32", False), (150, 8192, 9001, True, "f16", True, "f16", True)),
     ((200, 3072, 1000, False, "f16", False, "f16", False), (130, 3072, 1000, False, "f16", False, "f16", False)),
     ((300, 4096, 1001, True, "f32", False, "f32", True), (40, 4096, 1001, True, "f32", False, "f32", True)),
     ((64, 1001, 700, True, "f16", False, "f16", False), (33, 1001, 700, True, "f16", False, "f16", False)),

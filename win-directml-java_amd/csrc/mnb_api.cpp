@@ -75,6 +75,12 @@ hipError_t ensure(void **buf, size_t *cap, size_t bytes) {
     return e;
 }
 
+// Rows of x per launch of a product: at most 2 GiB of x (32-bit offsets),
+// a multiple of 128.
+static int64_t prefill_chunk_rows(int32_t ldx) {
+    return std::max<int64_t>(128, (((int64_t)1 << 31) / ((int64_t)ldx * 2)) / 128 * 128);
+}
+
 // IEEE binary32 -> binary16 bits, round to nearest even.
 uint16_t f32_to_f16_bits(float f) {
     uint32_t x;
@@ -173,10 +179,10 @@ int32_t mnb_context_create(int32_t device, mnb_context **out) {
         delete c;
         return hip_fail(e, "init");
     }
-    // the stream-K GEMM's partial-tile workspace (one workgroup per CU) is
+    // the stream-K GEMM's partial-tile workspace (for the largest grid) is
     // allocated here, so products on device pointers allocate nothing and can
     // be captured into a HIP graph from the first call
-    e = ensure(&c->sk_ws, &c->sk_ws_cap, mnb::sk_workspace_bytes(c->cu_count));
+    e = ensure(&c->sk_ws, &c->sk_ws_cap, mnb::sk_workspace_bytes(mnb::sk_max_grid(c->cu_count)));
     if (e != hipSuccess) {
         (void)hipStreamDestroy(c->stream);
         delete c;
@@ -582,6 +588,7 @@ int32_t mnb_supports_batch(const mnb_weight *w) { return w ? 1 : 0; }
 
 int32_t mnb_matmul_plan(const mnb_context *ctx, const mnb_weight *w, int32_t M, mnb_plan_info *out) {
     if (!ctx || !w) return fail(MNB_ERR_INVALID_STATE, "Kernel not prepared");
+    if (w->ctx != ctx) return fail(MNB_ERR_INVALID_ARGUMENT, "weight belongs to another context");
     if (!out) return fail(MNB_ERR_INVALID_ARGUMENT, "out must not be null");
     if (M < 1 || M > mnb_max_batch_rows()) return fail(MNB_ERR_INVALID_ARGUMENT, "M out of range [1, %d]: %d", mnb_max_batch_rows(), M);
     *out = mnb_plan_info{};
@@ -604,9 +611,7 @@ int32_t mnb_matmul_plan(const mnb_context *ctx, const mnb_weight *w, int32_t M, 
         return ok();
     }
     // the first chunk of x rows (see launch_prefill)
-    const int32_t ldx = (g.K + 7) & ~7;
-    const int64_t chunk_rows = std::max<int64_t>(128, (((int64_t)1 << 31) / ((int64_t)ldx * 2)) / 128 * 128);
-    const int32_t Mc = (int32_t)std::min<int64_t>(M, chunk_rows);
+    const int32_t Mc = (int32_t)std::min<int64_t>(M, prefill_chunk_rows((g.K + 7) & ~7));
     const mnb::ProductPlan pp = mnb::product_plan(g, Mc, ctx->cu_count);
     if (pp.ks) {
         out->kernel = MNB_KERNEL_KSLICE;
@@ -638,19 +643,32 @@ mnb::ProductPlan mnb::product_plan(const WeightGeom &g, int32_t M, int32_t cu_co
     return p;
 }
 
+size_t mnb::prefill_workspace_bytes(const WeightGeom &g, int32_t M, int32_t cu_count) {
+    if (M <= kSkinnyMaxM) return 0;
+    const int64_t chunk = std::min<int64_t>(M, prefill_chunk_rows((g.K + 7) & ~7));
+    size_t need = 0;
+    // every chunk but the last has `chunk` rows
+    for (const int64_t rows : {chunk, (int64_t)M % chunk}) {
+        if (rows <= 0) continue;
+        const ProductPlan pp = product_plan(g, (int32_t)rows, cu_count);
+        if (!pp.ks && !pp.sp.closed) need = std::max(need, sk_workspace_bytes(pp.sp.G));
+    }
+    return need;
+}
+
 // M > 16: per chunk of rows, the K-sliced kernel or the GEMM (stream-K over
 // one persistent workgroup per CU, or a closed-form tile list), whichever the
-// cost models expect to finish first.  ws holds the GEMM's partial tiles of
-// split tiles (sk_workspace_bytes(cu_count) bytes: the context's workspace,
-// allocated with it, or the fixed scratch array of mnb_matmul_noalloc).  The
+// cost models expect to finish first.  ws (ws_bytes bytes: the context's
+// workspace, allocated with it, or the fixed scratch array of
+// mnb_matmul_noalloc) holds the GEMM's partial tiles of split tiles and their
+// arrival counters; launch_gemm_sk refuses a grid it does not cover.  The
 // kernels address x and the scales with 32-bit byte offsets: rows of x go in
 // chunks of at most 2 GiB, and packed weights of 4 GiB or more are refused.
 static hipError_t launch_prefill(const mnb_weight *w, int cu_count, const mnb::MatmulArgs &a, float *ws,
-                                 hipStream_t s) {
+                                 size_t ws_bytes, hipStream_t s) {
     const mnb::WeightGeom &g = w->g;
     if ((uint64_t)g.NT * (uint64_t)g.ST * mnb::kTileBytes >= ((uint64_t)1 << 32)) return hipErrorInvalidValue;
-    const int64_t chunk_rows = std::max<int64_t>(128, (((int64_t)1 << 31) / ((int64_t)a.ldx * 2)) / 128 * 128);
-    const int chunk = (int)std::min<int64_t>(a.M, chunk_rows);
+    const int chunk = (int)std::min<int64_t>(a.M, prefill_chunk_rows(a.ldx));
     const size_t y_row = (size_t)g.N * (a.y_type == MNB_F16 ? 2 : 4);
     for (int m0 = 0; m0 < a.M; m0 += chunk) {
         mnb::MatmulArgs c = a;
@@ -661,7 +679,7 @@ static hipError_t launch_prefill(const mnb_weight *w, int cu_count, const mnb::M
         const mnb::SinglePlan &plan = pp.sp;
         const hipError_t e = pp.ks       ? mnb::launch_gemm_ks(w, c, pp.kc, s)
                              : plan.closed ? mnb::launch_gemm_closed(w, c, plan.ntw, plan.fm, plan.G, s)
-                                           : mnb::launch_gemm_sk(w, c, plan.G, ws, s);
+                                           : mnb::launch_gemm_sk(w, c, plan.G, ws, ws_bytes, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -694,7 +712,8 @@ size_t mnb::stage_x_bytes(const mnb_weight *w, int32_t M, const void *x, int32_t
 }
 
 hipError_t mnb::launch_product(const mnb_weight *w, int cu_count, int32_t M, const void *x, int32_t x_type, void *y,
-                               int32_t y_type, bool accumulate, void *stage_x, void *sk_ws, hipStream_t s) {
+                               int32_t y_type, bool accumulate, void *stage_x, void *sk_ws, size_t ws_bytes,
+                               hipStream_t s) {
     const WeightGeom &g = w->g;
     const int32_t ldx_pad = (g.K + 7) & ~7;
     mnb::MatmulArgs a;
@@ -711,7 +730,7 @@ hipError_t mnb::launch_product(const mnb_weight *w, int cu_count, int32_t M, con
     a.y = y;
     a.y_type = y_type;
     a.accumulate = accumulate ? 1 : 0;
-    if (M > mnb::kSkinnyMaxM) return launch_prefill(w, cu_count, a, (float *)sk_ws, s);
+    if (M > mnb::kSkinnyMaxM) return launch_prefill(w, cu_count, a, (float *)sk_ws, ws_bytes, s);
     // M <= 16: the K-sliced kernel where its cost model expects a clear gain
     // over the GEMV (9 <= M <= 16 and wide N)
     const mnb::KsPlan kp = mnb::ks_skinny_plan(g, M, cu_count);
@@ -746,8 +765,6 @@ int32_t mnb_matmul(mnb_context *ctx, const mnb_weight *w, int32_t M, const void 
     }
     const size_t stage = mnb::stage_x_bytes(w, M, xd, x_type);
     if (stage && (e = ensure(&ctx->stage_x, &ctx->stage_x_cap, stage)) != hipSuccess) return hip_fail(e, op);
-    if (M > mnb::kSkinnyMaxM && (e = ensure(&ctx->sk_ws, &ctx->sk_ws_cap, mnb::sk_workspace_bytes(ctx->cu_count))) != hipSuccess)
-        return hip_fail(e, op);
 
     void *yd = y;
     const size_t y_bytes = (size_t)MN * dtype_size(y_type);
@@ -760,7 +777,7 @@ int32_t mnb_matmul(mnb_context *ctx, const mnb_weight *w, int32_t M, const void 
     }
 
     e = mnb::launch_product(w, ctx->cu_count, M, xd, x_type, yd, y_type, (flags & MNB_ACCUMULATE) != 0, ctx->stage_x,
-                            ctx->sk_ws, s);
+                            ctx->sk_ws, ctx->sk_ws_cap, s);
     if (e != hipSuccess) return hip_fail(e, op);
 
     if (host) {
@@ -862,7 +879,7 @@ static int32_t group_create_gemm(mnb_context *ctx, int32_t count, const mnb_grou
     };
     if (!build(mnb::kGemmNTW)) return fail(MNB_ERR_INVALID_ARGUMENT, "group too large");
     plan.count = count;
-    plan.G = (int32_t)std::min<int64_t>(std::min(ctx->cu_count, 256), plan.iters);
+    plan.G = (int32_t)std::min<int64_t>(mnb::sk_max_grid(ctx->cu_count), plan.iters);
     // Tile-list order once every workgroup gets several whole tiles: the
     // workgroups of one XCD then run tiles that share x rows and weight
     // columns side by side, and no tile is split, so the 512-column kernel
@@ -1010,16 +1027,20 @@ int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *
     }
     if (items[0].M > mnb::kSkinnyMaxM) return group_create_gemm(ctx, count, items, out);
     // M == 1, and 2 <= M <= 4 (small-batch decode): the persistent streaming
-    // kernel with as many x rows per job as the group's largest M.
-    plan.stream_rows = plan.m1 ? 1 : plan.max_m <= 4 ? plan.max_m : 0;
+    // kernel with as many x rows per job as the group's largest M.  Its units
+    // code the n-tile in 16 bits, so a group with an item of more than 65536
+    // n-tiles (N > 1048576) runs on the GEMV group kernel instead.
+    bool stream_ok = true;
+    for (int32_t i = 0; i < count; ++i) stream_ok = stream_ok && items[i].weight->g.NT <= 65536;
+    plan.stream_rows = !stream_ok ? 0 : plan.m1 ? 1 : plan.max_m <= 4 ? plan.max_m : 0;
     // 4 < M <= 16 with many 32 x 512 tiles: the GEMM's weight stream (x
     // shared by the workgroup's waves in LDS, persistent workgroups) beats one
     // workgroup per n-tile, whose waves each read their own x rows.
-    if (plan.stream_rows == 0 && mnb::sk_wide_supported(plan.scale_f32, plan.sps)) {
+    if (plan.stream_rows == 0 && plan.max_m > 4 && mnb::sk_wide_supported(plan.scale_f32, plan.sps)) {
         int64_t skinny_tiles = 0;
         for (int32_t i = 0; i < count; ++i)
             skinny_tiles += mnb::sk_tiles(items[i].M, items[i].weight->g.NT, mnb::kGemmWideNTW, mnb::kGemmSkinnyFM);
-        if (skinny_tiles >= (int64_t)kGemmListTilesPerWg * std::min(ctx->cu_count, 256))
+        if (skinny_tiles >= (int64_t)kGemmListTilesPerWg * mnb::sk_max_grid(ctx->cu_count))
             return group_create_gemm(ctx, count, items, out);
     }
     if (wgs > std::numeric_limits<int32_t>::max()) return fail(MNB_ERR_INVALID_ARGUMENT, "group too large");
@@ -1037,9 +1058,6 @@ int32_t mnb_group_create(mnb_context *ctx, int32_t count, const mnb_group_item *
     std::vector<uint32_t> units;
     std::vector<int32_t> wave_begin;
     if (plan.stream_rows > 0) {
-        for (int32_t i = 0; i < count; ++i)
-            if (items[i].weight->g.NT > 65536)
-                return fail(MNB_ERR_UNSUPPORTED, "item %d: N=%d too large for a group", i, items[i].weight->g.N);
         const int wpc = mnb::stream_kernel_waves_per_cu(plan.scale_f32, plan.has_zp, plan.sps, plan.stream_rows);
         const int64_t total_waves = (int64_t)ctx->cu_count * wpc;
         plan.stream_wgs = (int32_t)(total_waves / mnb::kStreamWavesPerBlock);
@@ -1084,7 +1102,7 @@ int32_t mnb_group_run(mnb_context *ctx, const mnb_group *group, void *stream) {
     DeviceGuard guard(ctx->device);
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     if (group->gemm) {
-        const hipError_t e = mnb::launch_gemm_group(group->gplan, (float *)ctx->sk_ws, s);
+        const hipError_t e = mnb::launch_gemm_group(group->gplan, (float *)ctx->sk_ws, ctx->sk_ws_cap, s);
         if (e != hipSuccess) return hip_fail(e, "matmulBatch");
         return ok();
     }

@@ -72,9 +72,9 @@ constexpr int kSkHalfFM = kGemmHalfFM;       // half-height tiles (tile-list lau
 // rows padded to 80 bytes against bank conflicts.
 constexpr int kSkStageRow = 80, kSkStageWave = 32 * kSkStageRow, kSkStageBytes = kSkWaves * kSkStageWave;
 constexpr int kSkThreads = 64 * kSkWaves;
-constexpr int kSkPartialFloats = kSkBM * kSkBN;   // one fp32 partial tile, [kSkBM][kSkBN] row-major
+static_assert(kSkPartialFloats == kSkBM * kSkBN, "one fp32 partial tile, [kSkBM][kSkBN] row-major");
 constexpr int kSkReduceRows = 16;                 // rows of a partial tile per reduce workgroup
-constexpr int kSkReduceThreads = 256;             // each thread: 4 rows x 4 columns
+constexpr int kSkReduceThreads = kSkMaxGrid;      // each thread: 4 rows x 4 columns; one per contributor
 
 typedef float float16_t __attribute__((ext_vector_type(16)));
 // LDS staging of the epilogue is written in 8-byte and read in 16-byte
@@ -785,79 +785,6 @@ __global__ __launch_bounds__(kSkReduceThreads) void sk_reduce_kernel(SkParams p)
     }
 }
 
-size_t sk_workspace_bytes(int G) { return (size_t)G * 2 * kSkPartialFloats * sizeof(float); }
-
-int sk_tiles(int M, int NT, int ntw, int fm) {
-    const int bn = kSkWaves * ntw * kTileRows, bm = 32 * fm;
-    return ((M + bm - 1) / bm) * ((NT * kTileRows + bn - 1) / bn);
-}
-
-bool sk_wide_supported(int scale_f32, int sps) {
-    // a wave's scales of its four n-tiles must fit one 1 KiB window
-    return kSkWideNTW * kTileRows * sps * (scale_f32 ? 4 : 2) <= 1024;
-}
-
-// Estimated time of G workgroups (us).  A least-squares fit (4% median error)
-// to 300 timings on MI355X of the Phi-3 projections at M = 128, 512 and 2048
-// over every candidate G: a stage costs 1.16 us plus 0.38 us times the busy
-// fraction of the chip, each tile a workgroup touches 8.6 us (pipeline fill
-// and epilogue), and split tiles 0.28 us per MB of partial tiles (stored, then
-// read by the reduce kernel) less 2 us, plus 1.7 us when every CU holds a
-// split workgroup.
-static double sk_cost(int64_t T, int64_t ST, int64_t G, int cu_count) {
-    const int64_t I = T * ST;
-    const int64_t per_wg = (I + G - 1) / G;
-    bool split = false;
-    for (int64_t b = 1; b < G && !split; ++b) split = (b * I / G) % ST != 0;
-    const double load = (double)std::min<int64_t>(G, cu_count) / cu_count;
-    const double tiles = (double)((per_wg + ST - 1) / ST + (split ? 1 : 0));
-    double t = (double)per_wg * (1.16 + 0.38 * load) + 8.6 * tiles;
-    if (split) {
-        const double partial_mb = (double)(G + std::min<int64_t>(G, T)) * kSkPartialFloats * 4.0 / 1.0e6;
-        t += 0.28 * partial_mb - 2.0 + (G > cu_count - 8 ? 1.7 : 0.0);
-    }
-    return t;
-}
-
-// Candidates: every workgroup count that gives each workgroup whole tiles (G
-// dividing T), every tile cut into m equal pieces (G = m T), one workgroup per
-// CU, and two CUs per XCD fewer; the cheapest by sk_cost wins.  G never
-// exceeds the CU count (one persistent workgroup per CU) nor kSkReduceThreads
-// (one reduce thread per contributor).
-int sk_grid(int T, int ST, int cu_count) {
-    const int64_t I = (int64_t)T * ST;
-    const int64_t cap = std::min<int64_t>(std::min<int64_t>(cu_count, kSkReduceThreads), I);
-    int64_t best = 0;
-    double best_t = 0.0;
-    auto consider = [&](int64_t G) {
-        if (G < 1 || G > cap) return;
-        const double t = sk_cost(T, ST, G, cu_count);
-        if (best == 0 || t < best_t) best = G, best_t = t;
-    };
-    for (int64_t k = 1; k <= T; ++k)
-        if (T % k == 0) consider(T / k);
-    for (int64_t G = 2 * (int64_t)T; G <= cap; G += T) consider(G);
-    consider(cap);
-    consider(cap - 16);
-    return (int)best;
-}
-
-SinglePlan sk_single_plan(int M, int NT, int ST, int scale_f32, int sps, int cu_count) {
-    const int T = sk_tiles(M, NT);
-    SinglePlan plan{false, kSkNTW, kSkFM, sk_grid(T, ST, cu_count), 0.0};
-    const double stream_k = sk_cost(T, ST, plan.G, cu_count);
-    plan.est = stream_k;
-    if (!sk_wide_supported(scale_f32, sps)) return plan;
-    const int Tw = sk_tiles(M, NT, kSkWideNTW, kSkFM);
-    const int Gw = std::min(std::min(cu_count, kSkReduceThreads), Tw);
-    int busiest = 0;   // tiles of the busiest workgroup in closed-form order
-    for (int g = 0; g < Gw; ++g) busiest = std::max(busiest, sk_cf_first(Tw, Gw, g + 1) - sk_cf_first(Tw, Gw, g));
-    const double load = (double)Gw / cu_count;
-    const double wide = busiest * (ST * (1.16 + 0.38 * load) * kGemmWideStageCost + 8.6);
-    if (wide < stream_k) plan = SinglePlan{true, kSkWideNTW, kSkFM, Gw, wide};
-    return plan;
-}
-
 SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg, int ntw, int fm) {
     const WeightGeom &g = w->g;
     SkItem it{};
@@ -901,12 +828,16 @@ static void launch_sk_variant(int ntw, int fm, dim3 grid, dim3 block, hipStream_
 
 // Launches the GEMM over the items (count == 1: `one`, else the device table
 // `items` with host copy `host`) and, when some workgroup range boundary falls
-// inside a tile, the reduce kernel.
+// inside a tile, the reduce kernel.  A stream-K launch needs ws_bytes of at
+// least sk_workspace_bytes(G); else nothing is launched.
 static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem *host, int32_t count,
                             const SkTile *seq, const SkRange *wg, bool closed, int ntw, int fm, int64_t iters,
-                            int scale_f32, int has_zp, int sps, int G, float *ws, hipStream_t stream) {
-    if (iters >= (int64_t)1 << 31 || G < 1 || G > kSkReduceThreads) return hipErrorInvalidValue;
+                            int scale_f32, int has_zp, int sps, int G, float *ws, size_t ws_bytes, hipStream_t stream) {
+    if (iters >= (int64_t)1 << 31 || G < 1 || G > kSkMaxGrid) return hipErrorInvalidValue;
     if (closed && (count != 1 || seq)) return hipErrorInvalidValue;
+    // a stream-K launch may split tiles: the workspace must hold the partial
+    // tiles of its G workgroups
+    if (!seq && !closed && (!ws || ws_bytes < sk_workspace_bytes(G))) return hipErrorInvalidValue;
     // 256 x 128 tiles, or wide (512 x 128), half (512 x 64) and skinny (512 x 32) tiles in
     // tile-list order only (no split tiles, no partial tiles)
     const bool narrow = ntw == kSkNTW && fm == kSkFM;
@@ -957,23 +888,25 @@ static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem
     return e;
 }
 
-hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, hipStream_t stream) {
+hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, size_t ws_bytes,
+                          hipStream_t stream) {
     const WeightGeom &g = w->g;
     const SkItem one = sk_make_item(w, a, 0);
     return launch_sk(one, nullptr, &one, 1, nullptr, nullptr, false, kSkNTW, kSkFM, (int64_t)one.T * g.ST, g.scale_f32,
-                     g.has_zp, g.SPS, G, ws, stream);
+                     g.has_zp, g.SPS, G, ws, ws_bytes, stream);
 }
 
 hipError_t launch_gemm_closed(const mnb_weight *w, const MatmulArgs &a, int ntw, int fm, int G, hipStream_t stream) {
     const WeightGeom &g = w->g;
     const SkItem one = sk_make_item(w, a, 0, ntw, fm);
     return launch_sk(one, nullptr, &one, 1, nullptr, nullptr, true, ntw, fm, (int64_t)one.T * g.ST, g.scale_f32,
-                     g.has_zp, g.SPS, std::min(G, one.T), nullptr, stream);
+                     g.has_zp, g.SPS, std::min(G, one.T), nullptr, 0, stream);
 }
 
-hipError_t launch_gemm_group(const GemmGroupPlan &g, float *ws, hipStream_t stream) {
+hipError_t launch_gemm_group(const GemmGroupPlan &g, float *ws, size_t ws_bytes, hipStream_t stream) {
     return launch_sk(g.host[0], (const SkItem *)g.items, g.host.data(), g.count, (const SkTile *)g.seq,
-                     (const SkRange *)g.wg, false, g.ntw, g.fm, g.iters, g.scale_f32, g.has_zp, g.sps, g.G, ws, stream);
+                     (const SkRange *)g.wg, false, g.ntw, g.fm, g.iters, g.scale_f32, g.has_zp, g.sps, g.G, ws,
+                     ws_bytes, stream);
 }
 
 }  // namespace mnb

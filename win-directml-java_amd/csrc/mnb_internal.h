@@ -220,16 +220,6 @@ hipError_t launch_gemv_stream(const GemvGroupPlan &g, hipStream_t stream);
 int stream_kernel_waves_per_cu(int scale_f32, int has_zp, int sps, int rows);
 constexpr int kStreamWavesPerBlock = 4;
 
-// n-tiles (16 rows) per wave of the GEMM: 2 (256-column tiles), or 4
-// (512-column tiles, in tile-list order only); 32-row fragments per tile: 4
-// (128 rows), or 1 (32-row skinny tiles, with 512 columns, in tile-list
-// order only)
-constexpr int kGemmNTW = 2, kGemmWideNTW = 4;
-constexpr int kGemmFM = 4, kGemmHalfFM = 2, kGemmSkinnyFM = 1;
-// Cost of a 512-column stage in 256-column stages (same-box A/B of the M=512
-// group: 1046 vs 1155 TFLOP/s, so 2 / 1.105).
-constexpr double kGemmWideStageCost = 1.81;
-
 // A recorded group of independent products with M > 16 (all items share the
 // kernel variant): one launch over all their iterations, in stream-K order
 // (seq == nullptr) or in a tile list built at record time.
@@ -237,7 +227,7 @@ struct GemmGroupPlan {
     void *items = nullptr;          // device SkItem[count]
     void *seq = nullptr;            // device SkTile[tiles] (tile-list order)
     void *wg = nullptr;             // device SkRange[G + 1] (tile-list order)
-    std::vector<SkItem> host;       // host copy (split detection at launch)
+    std::vector<SkItem> host;       // host copy
     int32_t count = 0, G = 0;
     int32_t ntw = kGemmNTW;         // n-tiles per wave (kGemmWideNTW: tile-list order only)
     int32_t fm = kGemmFM;           // 32-row fragments per tile (kGemmSkinnyFM: tile-list order, wide)
@@ -246,35 +236,19 @@ struct GemmGroupPlan {
 };
 
 // Stream-K GEMM (M > 16): G persistent workgroups share the (tile, k-stage)
-// iterations; ws holds sk_workspace_bytes(G) of fp32 partial tiles for the
-// tiles whose stages span workgroups, which a second kernel on the same
-// stream sums in contributor order.
-size_t sk_workspace_bytes(int G);
-int sk_tiles(int M, int NT, int ntw = kGemmNTW, int fm = kGemmFM);
-// whether the weight variant has a 512-column kernel
-bool sk_wide_supported(int scale_f32, int sps);
-// Workgroup count for T tiles of ST stages on cu_count CUs (a cost model:
-// whole tiles per workgroup when that is cheapest, else stream-K).
-int sk_grid(int T, int ST, int cu_count);
-hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, hipStream_t stream);
+// iterations; the tiles whose stages span workgroups are written as fp32
+// partial tiles into ws (ws_bytes bytes, at least sk_workspace_bytes(G), else
+// hipErrorInvalidValue and nothing is launched), which a second kernel on the
+// same stream sums in contributor order.
+hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, size_t ws_bytes,
+                          hipStream_t stream);
 // One product in tile-list order with whole tiles of 32 fm rows x 128 ntw
 // columns on min(G, tiles) workgroups, the list in closed form (sk_cf_*): no
 // table, no split tile, no workspace.  Wide tiles (ntw = kGemmWideNTW) need
 // sk_wide_supported.
 hipError_t launch_gemm_closed(const mnb_weight *w, const MatmulArgs &a, int ntw, int fm, int G, hipStream_t stream);
-// How one product with M > 16 runs: stream-K over 128 x 256 tiles on sk_grid
-// workgroups, or whole 128 x 512 tiles in closed-form tile-list order when
-// the cost model of sk_grid, with a 512-column stage costing
-// kGemmWideStageCost 256-column stages, expects the busiest workgroup to
-// finish first that way.
-struct SinglePlan {
-    bool closed;
-    int ntw, fm, G;
-    double est;   // the cost model's time (us)
-};
-SinglePlan sk_single_plan(int M, int NT, int ST, int scale_f32, int sps, int cu_count);
 SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg, int ntw = kGemmNTW, int fm = kGemmFM);
-hipError_t launch_gemm_group(const GemmGroupPlan &g, float *ws, hipStream_t stream);
+hipError_t launch_gemm_group(const GemmGroupPlan &g, float *ws, size_t ws_bytes, hipStream_t stream);
 
 // One product with K sliced over the waves of each workgroup (single
 // products, M > 16): workgroup (m-block, n-group) owns 16 mb rows x 16 ntw
@@ -328,11 +302,16 @@ int32_t check_matmul(const mnb_context *ctx, const mnb_weight *w, int32_t M, con
 // and K is a multiple of 8 (the kernels read it in place), else M rows of K
 // rounded up to 8.
 size_t stage_x_bytes(const mnb_weight *w, int32_t M, const void *x, int32_t x_type);
+// Bytes of GEMM workspace the product of M > 16 rows needs: the largest
+// sk_workspace_bytes(G) over the stream-K grids of its row chunks (0 when no
+// chunk runs stream-K).
+size_t prefill_workspace_bytes(const WeightGeom &g, int32_t M, int32_t cu_count);
 // One product on device pointers: x staged into stage_x when stage_x_bytes
 // says so, then the GEMV (M <= 16) or the GEMM, whose split tiles use
-// sk_ws (sk_workspace_bytes(cu_count) bytes).  Allocates nothing.
+// sk_ws (ws_bytes bytes, at least sk_workspace_bytes(sk_max_grid(cu_count))).
+// Allocates nothing.
 hipError_t launch_product(const mnb_weight *w, int cu_count, int32_t M, const void *x, int32_t x_type, void *y,
-                          int32_t y_type, bool accumulate, void *stage_x, void *sk_ws, hipStream_t s);
+                          int32_t y_type, bool accumulate, void *stage_x, void *sk_ws, size_t ws_bytes, hipStream_t s);
 
 // largest M handled by the skinny (GEMV-style) kernel
 constexpr int kSkinnyMaxM = 16;

@@ -20,14 +20,14 @@
 
 namespace {
 
-// Partial tiles: two 128 x 256 fp32 tiles per workgroup of the largest GEMM
-// grid (256 workgroups), 64 MiB; staged x: 16 MiB of fp16.
-constexpr size_t kPartialBytes = (size_t)256 * 2 * 128 * 256 * 4;
+// Partial tiles of the largest GEMM grid (kSkMaxGrid workgroups: two
+// 128 x 256 fp32 tiles each, 64 MiB); staged x: 16 MiB of fp16.
+constexpr size_t kWorkspaceBytes = mnb::sk_workspace_bytes(mnb::kSkMaxGrid);
 constexpr size_t kStageBytes = (size_t)16 << 20;
 
 }  // namespace
 
-static __device__ __align__(256) unsigned char scratch[kPartialBytes + kStageBytes];
+static __device__ __align__(256) unsigned char scratch[kWorkspaceBytes + kStageBytes];
 
 namespace {
 
@@ -69,13 +69,18 @@ extern "C" int32_t mnb_matmul_noalloc(mnb_context *ctx, const mnb_weight *w, int
                  stage, kStageBytes);
         return mnb::report(MNB_ERR_INVALID_ARGUMENT, msg);
     }
-    if (M > mnb::kSkinnyMaxM && mnb::sk_workspace_bytes(ctx->cu_count < 256 ? ctx->cu_count : 256) > kPartialBytes)
-        return mnb::report(MNB_ERR_UNSUPPORTED, "partial tiles exceed mnb_matmul_noalloc's scratch array");
+    // the workspace of the grids this call will launch (the plan of every row chunk)
+    const size_t ws = mnb::prefill_workspace_bytes(w->g, M, ctx->cu_count);
+    if (ws > kWorkspaceBytes) {
+        snprintf(msg, sizeof msg, "the GEMM's partial tiles need %zu bytes, more than the %zu of mnb_matmul_noalloc's "
+                 "scratch array", ws, kWorkspaceBytes);
+        return mnb::report(MNB_ERR_UNSUPPORTED, msg);
+    }
     mnb::DeviceGuard guard(ctx->device);
     hipStream_t s = stream ? (hipStream_t)stream : ctx->stream;
     unsigned char *base = (unsigned char *)ctx->scratch;
     const hipError_t e = mnb::launch_product(w, ctx->cu_count, M, x, x_type, y, y_type, (flags & MNB_ACCUMULATE) != 0,
-                                             base + kPartialBytes, base, s);
+                                             base + kWorkspaceBytes, base, kWorkspaceBytes, s);
     if (e != hipSuccess) {
         snprintf(msg, sizeof msg, "MatMulNBitsKernel.%s failed: %s (%s)", M == 1 ? "matvec" : "matmulBatch",
                  hipGetErrorString(e), hipGetErrorName(e));

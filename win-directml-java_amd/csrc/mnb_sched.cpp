@@ -116,3 +116,78 @@ bool stream_schedule(const std::vector<int32_t> &NT, const std::vector<int32_t> 
 }
 
 }  // namespace mnb
+
+namespace mnb {
+
+int sk_tiles(int M, int NT, int ntw, int fm) {
+    const int bn = 8 * ntw * 16, bm = 32 * fm;   // 8 waves of 16 ntw columns, 32 fm rows
+    return ((M + bm - 1) / bm) * ((NT * 16 + bn - 1) / bn);
+}
+
+bool sk_wide_supported(int scale_f32, int sps) {
+    // a wave's scales of its four n-tiles (16 rows each) must fit one 1 KiB window
+    return kGemmWideNTW * 16 * sps * (scale_f32 ? 4 : 2) <= 1024;
+}
+
+// Estimated time of G workgroups (us).  A least-squares fit (4% median error)
+// to 300 timings on MI355X of the Phi-3 projections at M = 128, 512 and 2048
+// over every candidate G: a stage costs 1.16 us plus 0.38 us times the busy
+// fraction of the chip, each tile a workgroup touches 8.6 us (pipeline fill
+// and epilogue), and split tiles 0.28 us per MB of partial tiles (stored, then
+// read by the reduce kernel) less 2 us, plus 1.7 us when every CU holds a
+// split workgroup.
+static constexpr double kStageUs = 1.16, kStageBusyUs = 0.38, kTileUs = 8.6;
+
+double sk_cost(int64_t T, int64_t ST, int64_t G, int cu_count) {
+    const int64_t I = T * ST;
+    const int64_t per_wg = (I + G - 1) / G;
+    bool split = false;
+    for (int64_t b = 1; b < G && !split; ++b) split = (b * I / G) % ST != 0;
+    const double load = (double)std::min<int64_t>(G, cu_count) / cu_count;
+    const double tiles = (double)((per_wg + ST - 1) / ST + (split ? 1 : 0));
+    double t = (double)per_wg * (kStageUs + kStageBusyUs * load) + kTileUs * tiles;
+    if (split) {
+        const double partial_mb = (double)(G + std::min<int64_t>(G, T)) * kSkPartialFloats * 4.0 / 1.0e6;
+        t += 0.28 * partial_mb - 2.0 + (G > cu_count - 8 ? 1.7 : 0.0);
+    }
+    return t;
+}
+
+// Candidates: every workgroup count that gives each workgroup whole tiles (G
+// dividing T), every tile cut into m equal pieces (G = m T), one workgroup per
+// CU, and two CUs per XCD fewer; the cheapest by sk_cost wins.
+int sk_grid(int T, int ST, int cu_count) {
+    const int64_t I = (int64_t)T * ST;
+    const int64_t cap = std::min<int64_t>(sk_max_grid(cu_count), I);
+    int64_t best = 0;
+    double best_t = 0.0;
+    auto consider = [&](int64_t G) {
+        if (G < 1 || G > cap) return;
+        const double t = sk_cost(T, ST, G, cu_count);
+        if (best == 0 || t < best_t) best = G, best_t = t;
+    };
+    for (int64_t k = 1; k <= T; ++k)
+        if (T % k == 0) consider(T / k);
+    for (int64_t G = 2 * (int64_t)T; G <= cap; G += T) consider(G);
+    consider(cap);
+    consider(cap - 16);
+    return (int)best;
+}
+
+SinglePlan sk_single_plan(int M, int NT, int ST, int scale_f32, int sps, int cu_count) {
+    const int T = sk_tiles(M, NT);
+    SinglePlan plan{false, kGemmNTW, kGemmFM, sk_grid(T, ST, cu_count), 0.0};
+    const double stream_k = sk_cost(T, ST, plan.G, cu_count);
+    plan.est = stream_k;
+    if (!sk_wide_supported(scale_f32, sps)) return plan;
+    const int Tw = sk_tiles(M, NT, kGemmWideNTW, kGemmFM);
+    const int Gw = std::min(sk_max_grid(cu_count), Tw);
+    int busiest = 0;   // tiles of the busiest workgroup in closed-form order
+    for (int g = 0; g < Gw; ++g) busiest = std::max(busiest, sk_cf_first(Tw, Gw, g + 1) - sk_cf_first(Tw, Gw, g));
+    const double load = (double)Gw / cu_count;
+    const double wide = busiest * (ST * (kStageUs + kStageBusyUs * load) * kGemmWideStageCost + kTileUs);
+    if (wide < stream_k) plan = SinglePlan{true, kGemmWideNTW, kGemmFM, Gw, wide};
+    return plan;
+}
+
+}  // namespace mnb

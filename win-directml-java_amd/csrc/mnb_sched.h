@@ -2,6 +2,7 @@
 // side), free of HIP headers so the schedule builds and is checked on its own.
 #pragma once
 
+#include <stddef.h>
 #include <stdint.h>
 
 #include <vector>
@@ -103,6 +104,55 @@ MNB_HD inline int32_t sk_cf_tile(int32_t MT, int32_t NG, int32_t q) {
     const int32_t within = local - blk * mc * nb;
     return m0 + within / nn + (n0 + within % nn) * MT;
 }
+
+// ---- GEMM launch shapes and the single-product planner (host only) ----
+//
+// n-tiles (16 rows) per wave of the GEMM: 2 (256-column tiles), or 4
+// (512-column tiles, in tile-list order only); 32-row fragments per tile: 4
+// (128 rows), 2 (64-row tiles) or 1 (32-row tiles), both with 512 columns in
+// tile-list order only.
+constexpr int kGemmNTW = 2, kGemmWideNTW = 4;
+constexpr int kGemmFM = 4, kGemmHalfFM = 2, kGemmSkinnyFM = 1;
+// Cost of a 512-column stage in 256-column stages (same-box A/B of the M=512
+// group: 1046 vs 1155 TFLOP/s, so 2 / 1.105).
+constexpr double kGemmWideStageCost = 1.81;
+// One fp32 partial tile of a split 128 x 256 tile (floats).
+constexpr int kSkPartialFloats = 128 * 256;
+// Most workgroups of one GEMM launch: the partial-tile workspace (and the
+// fixed scratch array of mnb_matmul_noalloc) is sized for this many.
+constexpr int kSkMaxGrid = 256;
+
+// Output tiles of 32 fm rows x 128 ntw columns of an M x (16 NT) product.
+int sk_tiles(int M, int NT, int ntw = kGemmNTW, int fm = kGemmFM);
+// Whether the weight variant has a 512-column kernel: a wave's four n-tiles
+// of scales must fit one 1 KiB window.
+bool sk_wide_supported(int scale_f32, int sps);
+// Largest workgroup count of a GEMM launch on cu_count CUs: one persistent
+// workgroup per CU, at most kSkMaxGrid.  Every grid the planners pick is at
+// most this.
+inline int sk_max_grid(int cu_count) { return cu_count < kSkMaxGrid ? (cu_count < 1 ? 1 : cu_count) : kSkMaxGrid; }
+// Bytes of the stream-K workspace of a G-workgroup launch: two fp32 partial
+// tiles per workgroup (slot 0 for its first tile, 1 for its last).
+constexpr size_t sk_workspace_bytes(int G) { return (size_t)G * 2 * kSkPartialFloats * sizeof(float); }
+// Workgroup count for T tiles of ST stages on cu_count CUs (a cost model:
+// whole tiles per workgroup when that is cheapest, else stream-K with split
+// tiles summed by a reduce launch); at most sk_max_grid(cu_count) and at most
+// T * ST.
+int sk_grid(int T, int ST, int cu_count);
+// Estimated time (us) of T tiles of ST stages on G workgroups in stream-K
+// order (the model sk_grid minimises).
+double sk_cost(int64_t T, int64_t ST, int64_t G, int cu_count);
+// How one product with M > 16 runs on the GEMM: stream-K over 128 x 256
+// tiles on sk_grid workgroups, or whole 128 x 512 tiles in closed-form
+// tile-list order when the cost model, with a 512-column stage costing
+// kGemmWideStageCost 256-column stages, expects the busiest workgroup to
+// finish first that way.
+struct SinglePlan {
+    bool closed;
+    int ntw, fm, G;
+    double est;   // the cost model's time (us)
+};
+SinglePlan sk_single_plan(int M, int NT, int ST, int scale_f32, int sps, int cu_count);
 
 // The streaming kernel's unit of issue: up to kStreamJobTiles consecutive
 // super-tiles of one n-tile (a unit of ST super-tiles is stream_jobs(ST)
