@@ -29,6 +29,9 @@ M=512, Phi-3-mini shapes"):
 * phi3_export_variant: the same 129 Phi-3 projections in the weight format
   of the reference's DirectML int4 export (block size 128, explicit uint8
   zero points, fp16 scales) as one group launch at M=1 and at M=512.
+* ceilings: what the matrix cores sustain (an MFMA-only kernel at the GEMM's
+  occupancy, libmnb_probe.so) and hipBLASLt's dense fp16 GEMM of the same
+  129 projections as 129 launches, reference points for the prefill lines.
 * cpu_baseline: the oracle's restatement of the reference's Java CPU path
   (8-lane FMA block dot, one thread per core) on a bounded sample of the
   same decode step.
@@ -51,6 +54,7 @@ for _p in (os.path.join(ROOT, "win-directml-java_amd"), os.path.join(ROOT, "orac
 
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
+RIDGE_FLOP_PER_BYTE = FP16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
 BLOCK = 32
 
 
@@ -70,11 +74,13 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-sweep", action="store_true")
     p.add_argument("--eager", action="store_true", help="launch directly instead of via HIP graphs (counter runs)")
-    p.add_argument("--phase", choices=("all", "decode", "chain", "prefill", "qwen", "config0", "export"), default="all",
+    p.add_argument("--phase", choices=("all", "decode", "chain", "prefill", "qwen", "config0", "export", "ceilings"),
+                   default="all",
                    help="decode: only the M=1 group launch and the copy calibration; chain: only the 129 M=1 "
                         "launches in stream order (a HIP graph); prefill: only the M=512 launches (both for "
                         "counter runs); qwen: only the Qwen2.5-0.5B step at M=1 and 64; config0: only the single "
-                        "qkv product at M=1; export: only the Phi-3 step in the export's weight format")
+                        "qkv product at M=1; export: only the Phi-3 step in the export's weight format; "
+                        "ceilings: only the MFMA ceiling and the dense fp16 GEMM reference points")
     p.add_argument("--prefill-group", action="store_true",
                    help="with --phase prefill: the 129 projections as one group launch instead of 129 launches")
     p.add_argument("--prefill-m", type=int, default=512, help="with --phase prefill: rows M of the prefill step")
@@ -406,9 +412,15 @@ def phi3_export_variant(torch, mnb_hip, ctx, stream, args):
         with torch.cuda.stream(stream):
             grp.run(stream.cuda_stream)
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=stream):
-            grp.run(stream.cuda_stream)
+        if args.eager:
+            class _Direct:
+                def replay(self):
+                    grp.run(stream.cuda_stream)
+            g = _Direct()
+        else:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                grp.run(stream.cuda_stream)
         wall, gpu = time_graph(torch, g, stream, args.steps, args.warmup, args.settle_ms)
         del g
         grp.close()
@@ -459,9 +471,15 @@ def qwen_step(torch, mnb_hip, ctx, stream, args):
         with torch.cuda.stream(stream):
             grp.run(stream.cuda_stream)
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=stream):
-            grp.run(stream.cuda_stream)
+        if args.eager:
+            class _Direct:
+                def replay(self):
+                    grp.run(stream.cuda_stream)
+            g = _Direct()
+        else:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                grp.run(stream.cuda_stream)
         wall, gpu = time_graph(torch, g, stream, args.steps, args.warmup, args.settle_ms)
         del g
         grp.close()
@@ -469,11 +487,15 @@ def qwen_step(torch, mnb_hip, ctx, stream, args):
         flops = sum(2.0 * M * N * K for (_, _, K, N) in projs)
         e = {"us_per_step": round(wall * 1e6, 2), "gpu_us_per_step": round(gpu * 1e6, 2), "bytes_per_step": nbytes,
              "gbs": round(nbytes / wall / 1e9, 1), "tflops": round(flops / wall / 1e12, 2)}
+        # the roofline that bounds the step: HBM below the ridge (2.5 PFLOP/s /
+        # 8 TB/s = 312.5 flop per byte), MFMA above it; both fractions reported
+        e["flop_per_byte"] = round(flops / nbytes, 1)
+        e["bound"] = "hbm" if flops / nbytes < RIDGE_FLOP_PER_BYTE else "mfma"
+        e["frac_hbm_peak"] = round(nbytes / wall / 1e9 / HBM_PEAK_GBS, 4)
+        e["frac_fp16_peak"] = round(flops / wall / 1e12 / FP16_PEAK_TFLOPS, 4)
         if M == 1:
-            e["frac_hbm_peak"] = round(nbytes / wall / 1e9 / HBM_PEAK_GBS, 4)
             e["kernel"] = "mnb::gemv_stream_kernel (one launch per step)"
         else:
-            e["frac_fp16_peak"] = round(flops / wall / 1e12 / FP16_PEAK_TFLOPS, 4)
             e["kernel"] = "mnb::gemm_sk_kernel (one group launch per step)"
         out["m%d" % M] = e
         log("qwen step M=%d as one group launch: %.1f us, %.1f GB/s, %.1f TFLOP/s" % (M, wall * 1e6, e["gbs"],
@@ -482,6 +504,88 @@ def qwen_step(torch, mnb_hip, ctx, stream, args):
     for w in ws:
         w.close()
     return out
+
+
+def mfma_ceiling(torch, stream, settle_ms, launches=20):
+    """What the matrix cores sustain at the GEMM's occupancy: TFLOP/s of
+    libmnb_probe.so's MFMA-only kernel (v_mfma_f32_32x32x16_f16 on operands
+    drawn like the GEMM's, 256 workgroups of 8 waves, no memory traffic in
+    its loop), timed with HIP events on the launch stream after `settle_ms`
+    of untimed launches."""
+    lib = ctypes.CDLL(os.path.join(ROOT, "win-directml-java_amd", "mnb_hip", "libmnb_probe.so"))
+    lib.mnb_probe_mfma.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
+    lib.mnb_probe_mfma.restype = ctypes.c_int32
+    lib.mnb_probe_mfma_flops.argtypes = [ctypes.c_int32, ctypes.c_int32]
+    lib.mnb_probe_mfma_flops.restype = ctypes.c_double
+    wgs, iters = 256, 600
+    out = torch.empty(wgs * 512, dtype=torch.float32, device="cuda")
+    run = lambda n: lib.mnb_probe_mfma(wgs, iters, n, ctypes.c_void_p(out.data_ptr()),
+                                       ctypes.c_void_p(stream.cuda_stream))
+    assert run(1) == 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    assert run(4) == 0
+    torch.cuda.synchronize()
+    one = (time.perf_counter() - t0) / 4
+    assert run(int(max(1, settle_ms * 1e-3 / one))) == 0
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    assert run(launches) == 0
+    e1.record(stream)
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / launches
+    return lib.mnb_probe_mfma_flops(wgs, iters) / sec / 1e12, sec * 1e6
+
+
+def dense_fp16_gemm(torch, stream, projs, M, steps, warmup, settle_ms):
+    """The same projections as dense fp16 products through torch (hipBLASLt):
+    one fp16 weight [N, K] per projection (random, about 2 bytes per weight
+    where the int4 path streams about 0.56), x [M, K] fp16 per K, y fp16 per
+    N, 129 launches in stream order captured in a HIP graph; TFLOP/s of the
+    wall time per step.  A reference point for the single-product int4 path,
+    not part of it."""
+    gen = torch.Generator(device="cuda").manual_seed(4096)
+    ws = [torch.randn(N, K, device="cuda", dtype=torch.float16, generator=gen) * 0.05 for (_, _, K, N) in projs]
+    xs = {K: torch.randn(M, K, device="cuda", dtype=torch.float16, generator=gen) for (_, _, K, _) in projs}
+    ys = {N: torch.empty(M, N, device="cuda", dtype=torch.float16) for (_, _, _, N) in projs}
+    order = [(xs[K], w, ys[N]) for (_, _, K, N), w in zip(projs, ws)]
+
+    def run():
+        for x, w, y in order:
+            torch.mm(x, w.t(), out=y)
+    with torch.cuda.stream(stream):
+        run()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        run()
+    torch.cuda.synchronize()
+    wall, _ = time_graph(torch, g, stream, steps, warmup, settle_ms)
+    del g, ws, xs, ys, order
+    torch.cuda.empty_cache()
+    return sum(2.0 * M * N * K for (_, _, K, N) in projs) / wall / 1e12
+
+
+def ceilings(torch, stream, args):
+    """Reference points for the prefill GEMM's roofline fraction: the MFMA
+    ceiling the chip sustains, and hipBLASLt's dense fp16 GEMM of the same
+    129 Phi-3 projections as 129 launches (the single-product int4 path's
+    counterpart)."""
+    from mnb_hip import synth
+    tf, us = mfma_ceiling(torch, stream, args.settle_ms)
+    log("MFMA-only ceiling: %.1f TFLOP/s (%.1f us per launch)" % (tf, us))
+    projs = synth.phi3_decode_step()
+    dense = {}
+    for M in (512, 2048):
+        dense[str(M)] = round(dense_fp16_gemm(torch, stream, projs, M, max(3, args.steps // 4), 2, args.settle_ms), 1)
+        log("dense fp16 GEMM (hipBLASLt) of the 129 projections at M=%d as 129 launches: %.1f TFLOP/s" % (
+            M, dense[str(M)]))
+    return {"mfma_ceiling_tflops": round(tf, 1), "mfma_ceiling_frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4),
+            "mfma_ceiling_us_per_launch": round(us, 1),
+            "dense_fp16_gemm_tflops": dense,
+            "note": "mfma_ceiling: libmnb_probe.so, v_mfma_f32_32x32x16_f16 only, 256 workgroups of 8 waves; "
+                    "dense_fp16_gemm: torch.mm (hipBLASLt) of the same 129 Phi-3 projections with dense fp16 "
+                    "weights as 129 launches in a HIP graph"}
 
 
 def main():
@@ -505,6 +609,10 @@ def main():
     if args.phase == "export":
         print(json.dumps({"phase": "export", "phi3_export_variant": phi3_export_variant(torch, mnb_hip, ctx, stream, args)}),
               flush=True)
+        ctx.close()
+        return
+    if args.phase == "ceilings":
+        print(json.dumps({"phase": "ceilings", "ceilings": ceilings(torch, stream, args)}), flush=True)
         ctx.close()
         return
     if args.phase == "config0":
@@ -722,6 +830,8 @@ def main():
     qwen = qwen_step(torch, mnb_hip, ctx, stream, args)
     torch.cuda.empty_cache()
     export = phi3_export_variant(torch, mnb_hip, ctx, stream, args)
+    torch.cuda.empty_cache()
+    ceil = ceilings(torch, stream, args)
     ctx.close()
 
     cpu = None
@@ -769,7 +879,7 @@ def main():
                          "roofline": {"bound": "mfma", "achieved": round(kernel_tflops512, 2),
                                       "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                       "frac": round(kernel_tflops512 / FP16_PEAK_TFLOPS, 4),
-                                      "kernel": "mnb::gemm_sk_kernel + mnb::sk_reduce_kernel (one group launch per step)",
+                                      "kernel": "mnb::gemm_sk_kernel (one group launch per step: 128x512 tiles in tile-list order)",
                                       "avg_launch_us": round(gpu512 * 1e6, 2),
                                       "traffic": measured_traffic("gemm_sk_phi3_prefill_m512_group.md",
                                                                   "traffic_bytes_per_step"),
@@ -800,6 +910,7 @@ def main():
         "qwen_tied_lm_head": qwen_head,
         "qwen_step": qwen,
         "phi3_export_variant": export,
+        "ceilings": ceil,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
