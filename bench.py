@@ -149,6 +149,50 @@ def time_graph(torch, graph, stream, steps, warmup, settle_ms=0.0):
     return wall, gpu
 
 
+class _Direct:
+    """A step launched directly (counter runs: one dispatch per step, no graph)."""
+
+    def __init__(self, run):
+        self.replay = run
+
+
+def time_steps(torch, run, stream, steps, warmup, settle_ms=0.0, eager=False):
+    """Wall and GPU time per step of `run` (one step: its launches in stream
+    order).  The timed region is one replay of a HIP graph holding exactly
+    `steps` steps back to back, bracketed by two synchronizations and by HIP
+    events on the launch stream, so no host launch latency sits between two
+    steps (a graph of one short step replayed per step would time the host's
+    graph-launch rate, not the device).  Before it: `settle_ms` of untimed
+    replays of that graph and `warmup` single steps.  With eager, the steps are
+    launched directly (for counter runs)."""
+    with torch.cuda.stream(stream):
+        run()                   # eager run first (validates every call)
+    torch.cuda.synchronize()
+    if eager:
+        return time_graph(torch, _Direct(run), stream, steps, warmup, settle_ms)
+    gk = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gk, stream=stream):
+        for _ in range(steps):
+            run()
+    torch.cuda.synchronize()
+    settle(torch, gk, stream, settle_ms)
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            run()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        ev0.record(stream)
+        gk.replay()
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    gpu = ev0.elapsed_time(ev1) / 1e3 / steps
+    del gk
+    return wall, gpu
+
+
 def per_launch_times(torch, launcher, stream, reps=3):
     """Kernel duration of every launch (mean over reps), from a HIP event pair
     around it on the launch stream.  The stream is first held by a GPU sleep so
@@ -409,20 +453,8 @@ def phi3_export_variant(torch, mnb_hip, ctx, stream, args):
             xs = [xk[K] for (_, _, K, _) in projs]
         ys = [torch.empty(M, N, device="cuda", dtype=torch.float16) for (_, _, _, N) in projs]
         grp = mnb_hip.Group(ctx, list(zip(ws, xs, ys)))
-        with torch.cuda.stream(stream):
-            grp.run(stream.cuda_stream)
-        torch.cuda.synchronize()
-        if args.eager:
-            class _Direct:
-                def replay(self):
-                    grp.run(stream.cuda_stream)
-            g = _Direct()
-        else:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=stream):
-                grp.run(stream.cuda_stream)
-        wall, gpu = time_graph(torch, g, stream, args.steps, args.warmup, args.settle_ms)
-        del g
+        wall, gpu = time_steps(torch, lambda: grp.run(stream.cuda_stream), stream, args.steps, args.warmup,
+                               args.settle_ms, args.eager)
         grp.close()
         if M == 1:
             nbytes = sum(t.algorithmic_bytes(1) for t in host)
@@ -468,20 +500,8 @@ def qwen_step(torch, mnb_hip, ctx, stream, args):
             xs = [xk[K] for (_, _, K, _) in projs]
         ys = [torch.empty(M, N, device="cuda", dtype=torch.float16) for (_, _, _, N) in projs]
         grp = mnb_hip.Group(ctx, list(zip(ws, xs, ys)))
-        with torch.cuda.stream(stream):
-            grp.run(stream.cuda_stream)
-        torch.cuda.synchronize()
-        if args.eager:
-            class _Direct:
-                def replay(self):
-                    grp.run(stream.cuda_stream)
-            g = _Direct()
-        else:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=stream):
-                grp.run(stream.cuda_stream)
-        wall, gpu = time_graph(torch, g, stream, args.steps, args.warmup, args.settle_ms)
-        del g
+        wall, gpu = time_steps(torch, lambda: grp.run(stream.cuda_stream), stream, args.steps, args.warmup,
+                               args.settle_ms, args.eager)
         grp.close()
         nbytes = sum(t.algorithmic_bytes(M) for t in host)
         flops = sum(2.0 * M * N * K for (_, _, K, N) in projs)
@@ -660,25 +680,9 @@ def main():
         else:
             la = Launcher(ctx, weights, xs_l, ys_m, M, stream)
             run = la.run
-        if args.eager:
-            class _Direct:
-                def replay(self):
-                    run()
-            g = _Direct()
-        elif group:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.stream(stream):
-                run()           # eager run first
-            torch.cuda.synchronize()
-            with torch.cuda.graph(g, stream=stream):
-                run()
-            torch.cuda.synchronize()
-        else:
-            g = capture(torch, la, stream)
         steps = max(3, args.steps // 4) if M >= 512 and not group else args.steps
-        wall_m, gpu_m = time_graph(torch, g, stream, steps, 2, args.settle_ms)
+        wall_m, gpu_m = time_steps(torch, run, stream, steps, 2, args.settle_ms, args.eager)
         flops = sum(2.0 * M * N * K for (_, _, K, N) in projs)
-        del g
         if group:
             la.close()
             la = None
@@ -701,12 +705,10 @@ def main():
 
     if args.phase == "chain":
         dec = Launcher(ctx, weights, xs, ys, 1, stream)
-        g_dec = capture(torch, dec, stream)
-        wall_seq, gpu_seq = time_graph(torch, g_dec, stream, args.steps, args.warmup, args.settle_ms)
+        wall_seq, gpu_seq = time_steps(torch, dec.run, stream, args.steps, args.warmup, args.settle_ms, args.eager)
         print(json.dumps({"phase": "chain", "gbs": round(bytes_step / wall_seq / 1e9, 2),
                           "us_per_step": round(wall_seq * 1e6, 2), "gpu_us_per_step": round(gpu_seq * 1e6, 2),
                           "launches_per_step": len(projs), "bytes_per_step": bytes_step}), flush=True)
-        del g_dec
         for w in weights:
             w.close()
         ctx.close()
@@ -716,21 +718,9 @@ def main():
     #     dependence between them) recorded once as a group and run as one
     #     launch of the streaming kernel.
     grp = mnb_hip.Group(ctx, list(zip(weights, xs, ys)))
-    if args.eager:
-        class _Direct:
-            def replay(self):
-                grp.run(stream.cuda_stream)
-        g_grp = _Direct()
-    else:
-        g_grp = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(stream):
-            grp.run(stream.cuda_stream)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(g_grp, stream=stream):
-            grp.run(stream.cuda_stream)
-    wall, gpu = time_graph(torch, g_grp, stream, args.steps, args.warmup, args.settle_ms)
+    wall, gpu = time_steps(torch, lambda: grp.run(stream.cuda_stream), stream, args.steps, args.warmup,
+                           args.settle_ms, args.eager)
     value = bytes_step / wall / 1e9
-    del g_grp
     kern = group_launch_times(torch, grp, stream, reps=args.steps).mean()   # one launch per step
     achieved_gbs = bytes_step / kern / 1e9
     log("decode step as one group launch: %.1f us per step, %.1f us per launch (event brackets), %.1f GB/s" % (
@@ -750,10 +740,8 @@ def main():
     # (2) the same projections as 129 separate launches in stream order (each
     #     launch waits for the previous one, as in a dependent decode chain).
     dec = Launcher(ctx, weights, xs, ys, 1, stream)
-    g_dec = capture(torch, dec, stream)
-    wall_seq, gpu_seq = time_graph(torch, g_dec, stream, args.steps, args.warmup, args.settle_ms)
+    wall_seq, gpu_seq = time_steps(torch, dec.run, stream, args.steps, args.warmup, args.settle_ms, args.eager)
     log("decode step as 129 launches: %.1f us wall, %.1f GB/s" % (wall_seq * 1e6, bytes_step / wall_seq / 1e9))
-    del g_dec
     d1 = per_launch_times(torch, dec, stream)
     per_shape = {}
     for (name, layer, K, N), t, d in zip(projs, host, d1):
