@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <map>
 #include <set>
 #include <vector>
 
@@ -137,12 +138,79 @@ static int check_grid() {
     return 0;
 }
 
+// The reduce launch's split list against the partial tiles the GEMM writes:
+// for lines "G ST T [ST T ...]" (a stream-K launch of items with ST stages
+// and T tiles each), the GEMM's walk of each workgroup's range (segments of
+// one tile each; a segment shorter than its tile is written as a partial
+// tile, in slot 0 for the workgroup's first segment, else slot 1) must give,
+// for every split tile, exactly the contributors and slots that
+// mnb::sk_split_list lists, in workgroup order.
+static int check_split() {
+    char line[8192];
+    int cases = 0;
+    while (fgets(line, sizeof line, stdin)) {
+        std::vector<long> v;
+        for (char *tok = strtok(line, " \n"); tok; tok = strtok(nullptr, " \n")) v.push_back(atol(tok));
+        if (v.size() < 3 || v.size() % 2 == 0) continue;
+        const int G = (int)v[0];
+        std::vector<SkItem> items;
+        long ibeg = 0;
+        for (size_t i = 1; i + 1 < v.size(); i += 2) {
+            SkItem it{};
+            it.ST = (int32_t)v[i];
+            it.T = (int32_t)v[i + 1];
+            it.ibeg = (int32_t)ibeg;
+            ibeg += (long)it.ST * it.T;
+            items.push_back(it);
+        }
+        const long iters = ibeg;
+        if (G < 1 || G > kSkMaxGrid || G > iters) return fail("input", G, iters);
+        // the GEMM's partial tiles: key (item, tile) -> (workgroup, slot) in workgroup order
+        std::map<std::pair<int, long>, std::vector<std::pair<int, int>>> want;
+        for (int g = 0; g < G; ++g) {
+            long i = (long)g * iters / G;
+            const long i1 = (long)(g + 1) * iters / G;
+            bool first = true;
+            while (i < i1) {
+                int k = 0;
+                while (k + 1 < (int)items.size() && items[(size_t)k + 1].ibeg <= i) ++k;
+                const SkItem &it = items[(size_t)k];
+                const long t = (i - it.ibeg) / it.ST, ts = it.ibeg + t * it.ST;
+                const long end = std::min(i1, ts + it.ST);
+                if (end - i < it.ST) want[{k, t}].push_back({g, first ? 0 : 1});
+                first = false;
+                i = end;
+            }
+        }
+        SkSplitList list;
+        sk_split_list(items.data(), (int32_t)items.size(), iters, G, list);
+        if ((size_t)list.n != want.size()) return fail("split count", list.n, (long)want.size());
+        for (int j = 0; j < list.n; ++j) {
+            const SkSplit &e = list.e[j];
+            const long t = e.t_slot & 0x7fffffff;
+            const int slot0 = (int)((uint32_t)e.t_slot >> 31);
+            auto w = want.find({(int)e.item, t});
+            if (w == want.end()) return fail("unknown split tile", e.item, t);
+            if ((int)w->second.size() != e.g_last - e.g_first + 1) return fail("contributors", j, e.g_last - e.g_first + 1);
+            for (int c = 0; c < (int)w->second.size(); ++c) {
+                const int slot = c == 0 ? slot0 : 0;
+                if (w->second[(size_t)c].first != e.g_first + c || w->second[(size_t)c].second != slot)
+                    return fail("contributor slot", j, c);
+            }
+        }
+        ++cases;
+    }
+    printf("ok split cases=%d\n", cases);
+    return 0;
+}
+
 int main() {
     char first[32] = {0};
     if (scanf("%31s", first) != 1) return fail("input", 0, 0);
     if (strcmp(first, "stream") == 0) return check_stream();
     if (strcmp(first, "closed") == 0) return check_closed();
     if (strcmp(first, "grid") == 0) return check_grid();
+    if (strcmp(first, "split") == 0) return check_split();
     const int G = atoi(first);
     if (G < 1) return fail("input", G, 0);
     std::vector<SkItem> items;

@@ -171,3 +171,28 @@ def test_planner_grids_fit_the_workspace(checker):
                                                 rng.integers(0, 2), 2 ** rng.integers(0, 4)))
     r = subprocess.run([checker], input="grid\n" + "\n".join(lines) + "\n", capture_output=True, text=True)
     assert r.returncode == 0 and r.stdout.startswith("ok grid cases=%d" % len(lines)), r.stdout
+
+
+def test_reduce_split_list_matches_the_gemms_partial_tiles(checker):
+    """The split tiles the reduce launch sums (mnb::sk_split_list, built by the
+    host at launch time) are exactly the tiles the stream-K GEMM writes as
+    partial tiles, with the same contributors in the same order and the slot
+    each contributor writes: over the Phi-3 single products at M = 128, 512
+    and 2048 on the grids the planner picks, and 3000 random launches of 1 to
+    6 items on 1 to 256 workgroups."""
+    rng = np.random.default_rng(29)
+    lines = []
+    for M in (128, 512, 2048):
+        MT = (M + 127) // 128
+        for K, N in [(3072, 9216), (3072, 3072), (3072, 16384), (8192, 3072), (3072, 32064)]:
+            T, ST = MT * ((N + 255) // 256), (K + 127) // 128
+            for G in (T, min(256, T * ST), 240, 192, 144):
+                if 1 <= G <= min(256, T * ST):
+                    lines.append("%d %d %d" % (G, ST, T))
+    for _ in range(3000):
+        items = [(int(rng.integers(1, 71)), int(rng.integers(1, 61))) for _ in range(int(rng.integers(1, 7)))]
+        iters = sum(st * t for st, t in items)
+        G = int(rng.integers(1, min(256, iters) + 1))
+        lines.append("%d %s" % (G, " ".join("%d %d" % it for it in items)))
+    r = subprocess.run([checker], input="split\n" + "\n".join(lines) + "\n", capture_output=True, text=True)
+    assert r.returncode == 0 and r.stdout.startswith("ok split cases=%d" % len(lines)), r.stdout

@@ -74,7 +74,7 @@ constexpr int kSkStageRow = 80, kSkStageWave = 32 * kSkStageRow, kSkStageBytes =
 constexpr int kSkThreads = 64 * kSkWaves;
 static_assert(kSkPartialFloats == kSkBM * kSkBN, "one fp32 partial tile, [kSkBM][kSkBN] row-major");
 constexpr int kSkReduceRows = 16;                 // rows of a partial tile per reduce workgroup
-constexpr int kSkReduceThreads = kSkMaxGrid;      // each thread: 4 rows x 4 columns; one per contributor
+constexpr int kSkReduceThreads = 256;             // each thread: 4 rows x 4 columns
 
 typedef float float16_t __attribute__((ext_vector_type(16)));
 // LDS staging of the epilogue is written in 8-byte and read in 16-byte
@@ -723,34 +723,23 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
 }
 
 // Sums the partial tiles of every split tile in contributor order and writes
-// y.  Workgroup (b, rb) looks at the boundary between logical workgroups b
-// and b + 1 (b < G - 1); when that boundary falls inside tile t and is the
-// first boundary inside t, it reduces rows [rb * kSkReduceRows, +kSkReduceRows)
-// of t.  The contributors' partial-tile offsets are computed once per
-// workgroup into LDS; each thread owns four rows of one 4-column group and
-// keeps the loads of two contributors (eight 16-byte loads) in flight.
-__global__ __launch_bounds__(kSkReduceThreads) void sk_reduce_kernel(SkParams p) {
+// y.  Workgroup (j, rb) reduces rows [rb * kSkReduceRows, +kSkReduceRows) of
+// split tile j of the list; each thread owns four rows of one 4-column group
+// and keeps the loads of up to kBatch contributors (4 kBatch 16-byte loads)
+// in flight before it adds them in contributor order.
+__global__ __launch_bounds__(kSkReduceThreads) void sk_reduce_kernel(SkParams p, SkSplitList list) {
     constexpr int kRowBlocks = kSkBM / kSkReduceRows;
     constexpr int kColGroups = kSkBN / 4;
     constexpr int kRowsPerThread = kSkReduceRows * kColGroups / kSkReduceThreads;
-    __shared__ uint32_t s_part[kSkReduceThreads];   // partial-tile index (2 og + slot) of contributor i
-    const int b = (int)blockIdx.x / kRowBlocks + 1;   // boundary at sk_start(b)
+    constexpr int kRowStep = kSkReduceThreads / kColGroups;
+    constexpr int kBatch = 8;
+    const SkSplit e = list.e[blockIdx.x / kRowBlocks];
     const int rb = (int)blockIdx.x % kRowBlocks;
-    const int s = sk_start(b, p);
-    const SkItem it = sk_item(p, sk_find_item(p, s));
-    const int local = s - it.ibeg;
-    if (local % it.ST == 0) return;                   // between tiles: no split
-    const int t = local / it.ST;
-    const int ts = it.ibeg + t * it.ST;               // the tile's first iteration
-    if (sk_start(b - 1, p) > ts) return;              // an earlier boundary of t does the work
-    const int g_first = b - 1, g_last = sk_owner(ts + it.ST - 1, p);
-    const int nc = g_last - g_first + 1;              // contributors, at most G <= kSkReduceThreads
+    const int t = e.t_slot & 0x7fffffff;
+    const size_t slot0 = (uint32_t)e.t_slot >> 31;
+    const SkItem it = sk_item(p, e.item);
+    const int g_first = e.g_first, nc = (int)e.g_last - (int)e.g_first + 1;
     const int tid = (int)threadIdx.x;
-    if (tid < nc) {
-        const int og = g_first + tid;
-        s_part[tid] = (uint32_t)(og * 2 + (sk_start(og, p) >= ts ? 0 : 1));
-    }
-    __syncthreads();
     const int c = (tid % kColGroups) * 4;
     const int r0 = rb * kSkReduceRows + tid / kColGroups;
     const int m0 = (t % it.MT) * kSkBM, n = (t / it.MT) * kSkBN + c;
@@ -758,29 +747,28 @@ __global__ __launch_bounds__(kSkReduceThreads) void sk_reduce_kernel(SkParams p)
     // workgroup whose 16 rows all lie past M has nothing to do; in the block
     // that M cuts, the loads of rows past M read values that are never stored
     if (n >= it.N || m0 + rb * kSkReduceRows >= it.M) return;
-    float4_t sum[kRowsPerThread];
     auto part = [&](int i, int k) __attribute__((always_inline)) {
-        return gld((const float4_t *)(p.ws + (size_t)s_part[i] * kSkPartialFloats +
-                                       (r0 + k * (kSkReduceThreads / kColGroups)) * kSkBN + c));
+        const size_t pt = (size_t)(g_first + i) * 2 + (i == 0 ? slot0 : 0);
+        return gld((const float4_t *)(p.ws + pt * kSkPartialFloats + (size_t)(r0 + k * kRowStep) * kSkBN + c));
     };
-    int i = 0;
-    for (; i + 1 < nc; i += 2) {
-        float4_t a[kRowsPerThread], bb[kRowsPerThread];
+    float4_t sum[kRowsPerThread];
+    for (int i0 = 0; i0 < nc; i0 += kBatch) {
+        const int nb = min(kBatch, nc - i0);
+        float4_t v[kBatch][kRowsPerThread];
 #pragma unroll
-        for (int k = 0; k < kRowsPerThread; ++k) {
-            a[k] = part(i, k);
-            bb[k] = part(i + 1, k);
-        }
+        for (int j = 0; j < kBatch; ++j)
+            if (j < nb)
 #pragma unroll
-        for (int k = 0; k < kRowsPerThread; ++k) sum[k] = (i == 0 ? a[k] : sum[k] + a[k]) + bb[k];
-    }
-    if (i < nc) {
+                for (int k = 0; k < kRowsPerThread; ++k) v[j][k] = part(i0 + j, k);
 #pragma unroll
-        for (int k = 0; k < kRowsPerThread; ++k) sum[k] = sum[k] + part(i, k);   // nc >= 2, so i > 0 here
+        for (int j = 0; j < kBatch; ++j)
+            if (j < nb)
+#pragma unroll
+                for (int k = 0; k < kRowsPerThread; ++k) sum[k] = i0 + j == 0 ? v[j][k] : sum[k] + v[j][k];
     }
 #pragma unroll
     for (int k = 0; k < kRowsPerThread; ++k) {
-        const int m = m0 + r0 + k * (kSkReduceThreads / kColGroups);
+        const int m = m0 + r0 + k * kRowStep;
         if (m < it.M) store_y4(it, m, n, sum[k]);
     }
 }
@@ -871,18 +859,14 @@ static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem
 #undef MNB_SK_SPS
 #undef MNB_SK_LAUNCH
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || seq || closed) return e;
     // split tiles exist when some range boundary falls inside a tile (never
     // in tile-list order)
-    bool split = false;
-    int32_t k = 0;
-    for (int b = 1; b < G && !split && !seq && !closed; ++b) {
-        const int64_t s = (int64_t)b * iters / G;
-        while (k + 1 < count && host[k + 1].ibeg <= s) ++k;
-        split = (s - host[k].ibeg) % host[k].ST != 0;
-    }
-    if (split) {
-        hipLaunchKernelGGL(sk_reduce_kernel, dim3((G - 1) * (kSkBM / kSkReduceRows)), dim3(kSkReduceThreads), 0, stream, p);
+    SkSplitList list;
+    sk_split_list(host, count, iters, G, list);
+    if (list.n > 0) {
+        hipLaunchKernelGGL(sk_reduce_kernel, dim3(list.n * (kSkBM / kSkReduceRows)), dim3(kSkReduceThreads), 0, stream, p,
+                           list);
         e = hipGetLastError();
     }
     return e;

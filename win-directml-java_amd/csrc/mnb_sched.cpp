@@ -191,3 +191,29 @@ SinglePlan sk_single_plan(int M, int NT, int ST, int scale_f32, int sps, int cu_
 }
 
 }  // namespace mnb
+
+namespace mnb {
+
+void sk_split_list(const SkItem *host, int32_t count, int64_t iters, int G, SkSplitList &list) {
+    list.n = 0;
+    auto start = [&](int64_t g) { return g * iters / G; };
+    int32_t k = 0;
+    for (int b = 1; b < G && b <= kSkMaxSplits; ++b) {
+        const int64_t s = start(b);
+        while (k + 1 < count && host[k + 1].ibeg <= s) ++k;
+        const SkItem &it = host[k];
+        const int64_t local = s - it.ibeg;
+        if (local % it.ST == 0) continue;                // between tiles
+        const int64_t t = local / it.ST, ts = it.ibeg + t * it.ST;
+        if (start(b - 1) > ts) continue;                 // an earlier boundary lies inside t
+        int64_t g_last = b;                              // the owner of the tile's last iteration
+        while (g_last + 1 < G && start(g_last + 1) <= ts + it.ST - 1) ++g_last;
+        SkSplit &e = list.e[list.n++];
+        e.t_slot = (int32_t)((uint32_t)t | (start(b - 1) == ts ? 0u : 0x80000000u));
+        e.item = (uint16_t)k;
+        e.g_first = (uint8_t)(b - 1);
+        e.g_last = (uint8_t)g_last;
+    }
+}
+
+}  // namespace mnb

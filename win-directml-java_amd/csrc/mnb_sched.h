@@ -154,6 +154,27 @@ struct SinglePlan {
 };
 SinglePlan sk_single_plan(int M, int NT, int ST, int scale_f32, int sps, int cu_count);
 
+// The split tiles of one stream-K launch (the ranges of G logical
+// workgroups over `iters` iterations, range g = [g iters / G, (g + 1) iters /
+// G)), listed by the host at launch time and passed by value in the reduce
+// kernel's arguments, so nothing is allocated: tile t of item `item`, its
+// contributors g_first .. g_last (the workgroups whose ranges hold some of
+// its stages, in that order); g_first's partial tile is in its slot 0 when
+// the tile starts its range, else slot 1; the others' are in their slot 0.
+struct SkSplit {
+    int32_t t_slot;     // t | (slot of g_first's partial tile << 31)
+    uint16_t item;
+    uint8_t g_first, g_last;
+};
+constexpr int kSkMaxSplits = kSkMaxGrid - 1;   // at most one split tile per range boundary
+struct SkSplitList {
+    int32_t n;
+    SkSplit e[kSkMaxSplits];
+};
+// Fills `list` for items host[0 .. count) (ibeg ascending, iters in all,
+// G <= kSkMaxGrid): each split tile once, at the first range boundary inside it.
+void sk_split_list(const SkItem *host, int32_t count, int64_t iters, int G, SkSplitList &list);
+
 // The streaming kernel's unit of issue: up to kStreamJobTiles consecutive
 // super-tiles of one n-tile (a unit of ST super-tiles is stream_jobs(ST)
 // jobs; the last job of a unit whose ST is not a multiple loads its last
