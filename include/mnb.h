@@ -285,6 +285,8 @@ int32_t mnb_group_destroy(mnb_group *group);
 #define MNB_ORDER_NONE 0         /* one unit of work per workgroup or a static unit list */
 #define MNB_ORDER_STREAM_K 1     /* (tile, k-stage) iterations cut into equal ranges; split tiles reduced after */
 #define MNB_ORDER_TILE_LIST 2    /* whole tiles per workgroup from a tile list (a table, or closed form for one product) */
+#define MNB_ORDER_TILE_LIST_PARTS 3 /* a group's tile list whose longest tiles are cut along K into parts (fp32 partial
+                                       tiles, summed in K order by a reduce launch after) */
 typedef struct mnb_plan_info {
     int32_t kernel;      /* MNB_KERNEL_* */
     int32_t order;       /* MNB_ORDER_* */

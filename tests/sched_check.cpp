@@ -4,7 +4,8 @@
 //   streaming M = 1 schedule (mnb::stream_schedule): the word "stream", the
 //     wave count, then one line "NT ST" per item;
 //   closed-form tile list of a single item (mnb::sk_cf_*): the word "closed",
-//     then lines "G MT NG ST", each checked against sk_tile_list of that item.
+//     then lines "G MT NG ST", each checked against sk_tile_list of that item;
+//   "grid", "split" and "parts": see check_grid, check_split, check_parts.
 // Exits 1 on the first broken invariant; prints balance (and, for the tile
 // list, locality) figures.
 #include <stdio.h>
@@ -187,20 +188,129 @@ static int check_split() {
         if ((size_t)list.n != want.size()) return fail("split count", list.n, (long)want.size());
         for (int j = 0; j < list.n; ++j) {
             const SkSplit &e = list.e[j];
-            const long t = e.t_slot & 0x7fffffff;
+            const long t = e.t_slot & kSkSplitTile;
             const int slot0 = (int)((uint32_t)e.t_slot >> 31);
+            if ((uint32_t)e.t_slot & kSkSplitParts) return fail("parts flag in a stream-K list", j, t);
             auto w = want.find({(int)e.item, t});
             if (w == want.end()) return fail("unknown split tile", e.item, t);
-            if ((int)w->second.size() != e.g_last - e.g_first + 1) return fail("contributors", j, e.g_last - e.g_first + 1);
+            if ((int)w->second.size() != e.last - e.first + 1) return fail("contributors", j, e.last - e.first + 1);
             for (int c = 0; c < (int)w->second.size(); ++c) {
                 const int slot = c == 0 ? slot0 : 0;
-                if (w->second[(size_t)c].first != e.g_first + c || w->second[(size_t)c].second != slot)
+                if (w->second[(size_t)c].first != e.first + c || w->second[(size_t)c].second != slot)
                     return fail("contributor slot", j, c);
             }
         }
         ++cases;
     }
     printf("ok split cases=%d\n", cases);
+    return 0;
+}
+
+// Tile lists with parts (mnb::sk_tile_list_parts): for lines "G split_above
+// MT NG ST [MT NG ST ...]", every tile of every item is covered exactly once:
+// whole (stages 0 .. ST, no partial) when ST <= split_above, else by
+// ceil(ST / split_above) parts whose stage ranges tile [0, ST) in K order,
+// each shorter than split_above + 1, with consecutive partial indices that
+// the reduce list names (tile, item, first .. last, parts flag); the
+// workgroup ranges agree with the listed stages; and the busiest workgroup
+// exceeds the mean by less than the longest unit.  Prints per line the
+// busiest workgroup's stages with and without parts.
+static int check_parts() {
+    char line[8192];
+    int cases = 0;
+    while (fgets(line, sizeof line, stdin)) {
+        std::vector<long> v;
+        for (char *tok = strtok(line, " \n"); tok; tok = strtok(nullptr, " \n")) v.push_back(atol(tok));
+        if (v.size() < 5 || (v.size() - 2) % 3 != 0) continue;
+        const int G = (int)v[0];
+        const long split = v[1];
+        std::vector<SkItem> items;
+        long ibeg = 0;
+        for (size_t i = 2; i + 2 < v.size(); i += 3) {
+            SkItem it{};
+            it.MT = (int32_t)v[i];
+            it.T = (int32_t)(v[i] * v[i + 1]);
+            it.ST = (int32_t)v[i + 2];
+            it.ibeg = (int32_t)ibeg;
+            ibeg += (long)it.T * it.ST;
+            items.push_back(it);
+        }
+        const long iters = ibeg;
+        std::vector<SkTile> seq, seq0;
+        std::vector<SkRange> wg, wg0;
+        SkSplitList list;
+        if (!sk_tile_list_parts(items, G, split, seq, wg, list)) {
+            printf("refused %d\n", cases);
+            ++cases;
+            continue;
+        }
+        sk_tile_list(items, G, seq0, wg0);
+        // coverage: per (item, tile) the stage ranges, in the order listed
+        std::map<std::pair<int, long>, std::vector<SkTile>> got;
+        for (const SkTile &e : seq) {
+            if (e.item < 0 || e.item >= (int)items.size()) return fail("item index", e.item, (long)items.size());
+            if (e.t < 0 || e.t >= items[(size_t)e.item].T) return fail("tile index", e.t, items[(size_t)e.item].T);
+            got[{e.item, (long)e.t}].push_back(e);
+        }
+        long tiles = 0;
+        for (const SkItem &it : items) tiles += it.T;
+        if ((long)got.size() != tiles) return fail("tiles covered", (long)got.size(), tiles);
+        std::vector<char> part_seen((size_t)kSkMaxParts, 0);
+        int cut = 0;
+        long longest = 0;
+        for (auto &kv : got) {
+            const SkItem &it = items[(size_t)kv.first.first];
+            std::vector<SkTile> &ps = kv.second;
+            std::sort(ps.begin(), ps.end(), [](const SkTile &a, const SkTile &b) { return a.st0 < b.st0; });
+            const long np = split > 0 && it.ST > split ? (it.ST + split - 1) / split : 1;
+            if ((long)ps.size() != np) return fail("parts of a tile", (long)ps.size(), np);
+            long s0 = 0;
+            for (size_t j = 0; j < ps.size(); ++j) {
+                const SkTile &e = ps[j];
+                if (e.st0 != s0 || e.nst < 1) return fail("stage ranges", e.st0, s0);
+                if (np > 1 && e.nst > split) return fail("part longer than split", e.nst, split);
+                if (np == 1 && e.part != -1) return fail("whole tile with a partial", e.part, 0);
+                if (np > 1) {
+                    if (e.part < 0 || e.part >= kSkMaxParts || part_seen[(size_t)e.part]++) return fail("part index", e.part, 0);
+                    if (e.part != ps[0].part + (int)j) return fail("part indices not consecutive", e.part, ps[0].part);
+                }
+                s0 += e.nst;
+                longest = std::max<long>(longest, e.nst);
+            }
+            if (s0 != it.ST) return fail("stages covered", s0, it.ST);
+            if (np > 1) {
+                // the reduce list names this tile once, with its parts in K order
+                int found = 0;
+                for (int j = 0; j < list.n; ++j) {
+                    const SkSplit &e = list.e[j];
+                    if (!((uint32_t)e.t_slot & kSkSplitParts) || ((uint32_t)e.t_slot & kSkSplitSlot1)) return fail("flags", j, 0);
+                    if (e.item == kv.first.first && (long)(e.t_slot & kSkSplitTile) == kv.first.second) {
+                        ++found;
+                        if (e.first != ps[0].part || e.last != ps.back().part) return fail("list parts", e.first, ps[0].part);
+                    }
+                }
+                if (found != 1) return fail("cut tile listed", found, 1);
+                ++cut;
+            }
+        }
+        if (cut != list.n) return fail("list length", list.n, cut);
+        // workgroup ranges
+        if ((int)wg.size() != G + 1 || wg[0].pos != 0 || wg[0].iter != 0) return fail("wg[0]", wg[0].pos, wg[0].iter);
+        if (wg[(size_t)G].pos != (long)seq.size() || wg[(size_t)G].iter != iters) return fail("wg[G]", wg[(size_t)G].pos, iters);
+        long busiest = 0, busiest0 = 0;
+        for (int g = 0; g < G; ++g) {
+            long st = 0;
+            for (int k = wg[(size_t)g].pos; k < wg[(size_t)g + 1].pos; ++k) st += seq[(size_t)k].nst;
+            if (st != wg[(size_t)g + 1].iter - wg[(size_t)g].iter) return fail("wg stages", g, st);
+            busiest = std::max(busiest, st);
+            busiest0 = std::max<long>(busiest0, wg0[(size_t)g + 1].iter - wg0[(size_t)g].iter);
+        }
+        // the deal's bound (per XCD chunk, with each unit's epilogue cost of 2 stages)
+        if ((double)busiest > (double)iters / G * 1.15 + longest + 2 * 8) return fail("balance", busiest, iters / G);
+        printf("ok parts busiest=%ld unsplit=%ld mean=%.1f cut=%d\n", busiest, busiest0, (double)iters / G, cut);
+        ++cases;
+    }
+    printf("ok parts cases=%d\n", cases);
     return 0;
 }
 
@@ -211,6 +321,7 @@ int main() {
     if (strcmp(first, "closed") == 0) return check_closed();
     if (strcmp(first, "grid") == 0) return check_grid();
     if (strcmp(first, "split") == 0) return check_split();
+    if (strcmp(first, "parts") == 0) return check_parts();
     const int G = atoi(first);
     if (G < 1) return fail("input", G, 0);
     std::vector<SkItem> items;

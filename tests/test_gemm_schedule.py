@@ -8,8 +8,9 @@ dispatches (INT4_MATMUL_BATCH_TILED_HLSL, MatMulNBitsKernel.java:732-820,
 one per projection); the reference has no counterpart of this schedule, so
 what is pinned here are its invariants: every output tile of every item is
 computed exactly once, each workgroup's iteration range equals the stages of
-its own tiles (so no tile is split and no partial sums are needed), the
-ranges tile the launch, and the per-workgroup work is balanced."""
+its own tiles, the ranges tile the launch, and the per-workgroup work is
+balanced; a tile list with parts covers each cut tile's stages exactly once,
+in K order, with the partial tiles the reduce list names."""
 import os
 import re
 import subprocess
@@ -56,7 +57,7 @@ def test_phi3_step_groups(checker, M):
 
 
 def test_tile_list_group_of_the_gpu_test(checker):
-    specs = [(512, 3072, 9216), (700, 576, 8000), (2048, 1536, 3072), (300, 8192, 5000), (4500, 256, 1100),
+    specs = [(512, 3072, 9216), (700, 576, 8000), (2048, 1536, 3072), (300, 2048, 5000), (4500, 256, 1100),
              (129, 3072, 16384), (64, 200, 30000), (1024, 1024, 4096)]
     items = [((M + 127) // 128, (N + 255) // 256, (((K + 31) // 32) * 32 + 127) // 128) for M, K, N in specs]
     f = run(checker, 256, items)
@@ -70,6 +71,64 @@ def test_random_groups(checker, seed):
     n = int(rng.integers(1, 40))
     items = [(int(rng.integers(1, 41)), int(rng.integers(1, 131)), int(rng.integers(1, 71))) for _ in range(n)]
     run(checker, G, items)
+
+
+def run_parts(checker, lines):
+    """lines: (G, split_above, [(MT, NG, ST), ...]) per case.  Returns the
+    checker's output lines (one per case, then a summary)."""
+    inp = "parts\n" + "".join("%d %d " % (G, split) + " ".join("%d %d %d" % t for t in items) + "\n"
+                              for G, split, items in lines)
+    r = subprocess.run([checker], input=inp, capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    return r.stdout.splitlines()
+
+
+def qwen_m64():
+    """The Qwen2.5-0.5B step's 97 projections at M = 64 in 64 x 512 tiles."""
+    layer = [(896, 1152), (896, 896), (896, 9728), (4864, 896)]
+    return [(1, (N + 511) // 512, (K + 127) // 128) for _ in range(24) for K, N in layer] + \
+        [(1, (151936 + 511) // 512, 7)]
+
+
+def test_tile_list_parts_of_the_qwen_step_at_m64(checker):
+    """The down tiles (38 stages) against a mean of 31 stages per workgroup:
+    cut into two parts each, the busiest workgroup falls from 38 to 35 stages
+    (the rest is the 7-stage tiles' granularity)."""
+    items = qwen_m64()
+    iters = sum(a * b * c for a, b, c in items)
+    mean = -(-iters // 256)
+    out = run_parts(checker, [(256, 0, items), (256, mean, items)])
+    whole = dict(re.findall(r"(\w+)=([\d.]+)", out[0]))
+    cut = dict(re.findall(r"(\w+)=([\d.]+)", out[1]))
+    assert int(whole["busiest"]) == 38 and int(whole["cut"]) == 0
+    assert int(cut["cut"]) == 48 and int(cut["busiest"]) <= 35
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_tile_list_parts_random(checker, seed):
+    """Random groups and cut lengths: coverage of every tile's stages by its
+    parts in K order, consecutive partial indices named by the reduce list,
+    workgroup ranges, balance; or a refusal when the parts would exceed the
+    workspace's partial tiles or the list."""
+    rng = np.random.default_rng(1000 + seed)
+    cases = []
+    for _ in range(4):
+        G = int(rng.choice([1, 8, 40, 128, 256]))
+        n = int(rng.integers(1, 12))
+        items = [(int(rng.integers(1, 5)), int(rng.integers(1, 60)), int(rng.integers(1, 90))) for _ in range(n)]
+        cases.append((G, int(rng.integers(0, 40)), items))
+    out = run_parts(checker, cases)
+    assert out[-1] == "ok parts cases=%d" % len(cases)
+    assert all(l.startswith("ok parts busiest=") or l.startswith("refused") for l in out[:-1])
+
+
+def test_tile_list_parts_refused_beyond_the_list(checker):
+    """More than 256 partial tiles (300 or 129 tiles of 2 parts, 64 tiles of
+    10): refused, so the planner keeps whole tiles; 128 tiles of 2 parts fit."""
+    out = run_parts(checker, [(256, 10, [(1, 300, 20)]), (256, 10, [(1, 128, 20)]), (256, 2, [(1, 64, 20)]),
+                              (256, 10, [(1, 129, 20)])])
+    assert out[0].startswith("refused") and out[1].startswith("ok parts") and out[2].startswith("refused")
+    assert out[3].startswith("refused")
 
 
 def test_more_workgroups_than_tiles(checker):

@@ -545,20 +545,22 @@ def test_group_matches_oracle_and_single_launches(ctx):
 GEMM, GEMV_GROUP, KSLICE = mnb_hip.MNB_KERNEL_GEMM, mnb_hip.MNB_KERNEL_GEMV_GROUP, mnb_hip.MNB_KERNEL_KSLICE
 STREAM = mnb_hip.MNB_KERNEL_STREAM
 STREAM_K, TILE_LIST, NO_ORDER = mnb_hip.MNB_ORDER_STREAM_K, mnb_hip.MNB_ORDER_TILE_LIST, mnb_hip.MNB_ORDER_NONE
+PARTS = mnb_hip.MNB_ORDER_TILE_LIST_PARTS
 
 
-def _check_prefill_group(ctx, specs, seed, bs=32, plan=None):
+def _check_prefill_group(ctx, specs, seed, bs=32, plan=None, f32_scales=False):
     """Records the products `specs` (M, K, N, y dtype, y +=) as groups (one
     per accumulate flag) and checks every item against the oracle on sampled
     rows and against its own single launch, with replays bitwise identical.
     `plan` (kernel, order, tile rows, tile columns) is the schedule every
-    group must have recorded (mnb_group_plan)."""
+    group must have recorded (mnb_group_plan); `f32_scales` uploads the
+    scales as fp32 (the same values)."""
     import torch
     entries, host = [], []
     st = torch.cuda.Stream()
     for i, (M, K, N, ydt, acc) in enumerate(specs):
         t = synth.make_weight(seed + i, N, K, bs, with_zp=True)
-        w = upload(ctx, t)
+        w = upload(ctx, t, as_f32_scales=f32_scales)
         x16 = synth.make_x(seed + 100 + i, M, K)
         y0 = np.random.default_rng(seed + 200 + i).standard_normal((M, N)).astype(ydt)
         entries.append((w, torch.from_numpy(x16).cuda(), torch.from_numpy(y0.copy()).cuda()))
@@ -620,9 +622,10 @@ def test_group_of_prefill_products_in_tile_list_order(ctx):
     256-CU device) runs in tile-list order: whole tiles per workgroup, blocks
     of tiles that share x rows and weight columns side by side on one XCD.
     Items cover one to 36 m-tiles, k tails (K = 200, 576), N tails and fp16
-    and fp32 outputs."""
+    and fp32 outputs; no tile is longer than a workgroup's mean share, so
+    none is cut into parts."""
     specs = [(512, 3072, 9216, np.float16, False), (700, 576, 8000, np.float32, False),
-             (2048, 1536, 3072, np.float16, False), (300, 8192, 5000, np.float16, False),
+             (2048, 1536, 3072, np.float16, False), (300, 2048, 5000, np.float16, False),
              (4500, 256, 1100, np.float32, False), (129, 3072, 16384, np.float16, False),
              (64, 200, 30000, np.float16, False), (1024, 1024, 4096, np.float32, False)]
     tiles = sum(((M + 127) // 128) * ((N + 255) // 256) for M, K, N, _, _ in specs)
@@ -807,6 +810,40 @@ def test_group_of_short_products_with_32_row_tiles(ctx):
              (24, 128, 250000, np.float16, False)]
     assert sum((N + 511) // 512 for M, K, N, _, _ in specs) == 1173
     for w, _, _ in _check_prefill_group(ctx, specs, 2400, plan=(GEMM, TILE_LIST, 32, 512)):
+        w.close()
+
+
+def test_group_with_long_tiles_cut_into_parts_64_row(ctx):
+    """64-row tiles in a tile list whose long tiles (K = 4864: 38 stages,
+    against a mean of 5 to 7 per workgroup) are cut along K into parts: the
+    parts write fp32 partial tiles and the reduce launch sums them in K order
+    into y; rows past M (M = 48, 40), N tails, fp16 and fp32 outputs, and y +=
+    (the reduce adds y once).  The short items' whole tiles write y
+    directly in the same launch."""
+    specs = [(64, 512, 200000, np.float16, False), (48, 4864, 1000, np.float32, False),
+             (64, 4864, 896, np.float16, False), (40, 4864, 1000, np.float16, True),
+             (64, 512, 150000, np.float32, True)]
+    for w, _, _ in _check_prefill_group(ctx, specs, 2800, plan=(GEMM, PARTS, 64, 512)):
+        w.close()
+
+
+def test_group_with_long_tiles_cut_into_parts_32_row(ctx):
+    """32-row tiles (16 < M <= 32) with parts: K = 4864 and 8192 items (38 and
+    64 stages) among 1172 two-stage tiles; M = 17 and 24 ragged."""
+    specs = [(32, 256, 600000, np.float16, False), (17, 4864, 1000, np.float32, False),
+             (24, 8192, 3072, np.float16, False)]
+    for w, _, _ in _check_prefill_group(ctx, specs, 2900, plan=(GEMM, PARTS, 32, 512)):
+        w.close()
+
+
+def test_group_with_long_tiles_cut_into_parts_128_row(ctx):
+    """128 x 256 tiles in a tile list with parts (fp32 scales at bs 16 have
+    no 512-column kernel): K = 4864 and 8192 items with two m-tiles (M = 200,
+    130: rows past M in the second) among 1024 two-stage tiles."""
+    specs = [(128, 256, 262000, np.float16, False), (200, 4864, 1000, np.float32, False),
+             (130, 8192, 512, np.float16, False)]
+    assert sum(((M + 127) // 128) * ((N + 255) // 256) for M, K, N, _, _ in specs) == 1036
+    for w, _, _ in _check_prefill_group(ctx, specs, 3000, bs=16, plan=(GEMM, PARTS, 128, 256), f32_scales=True):
         w.close()
 
 

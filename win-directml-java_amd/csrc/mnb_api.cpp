@@ -832,6 +832,10 @@ constexpr int kGemmSkinnyMaxM = 32, kGemmHalfMaxM = 64;
 // Cost of a 64 x 512 stage in 128 x 256 stages: the same MFMA work and the
 // same operand bytes (x and weights trade places), rounded up.
 constexpr double kGemmHalfStageCost = 1.1;
+// Cost of the reduce launch after a tile list with parts, in stages of the
+// busiest workgroup (a launch and the partial tiles read back: ~4 us against
+// ~2.5 us per 64 x 512 stage).
+constexpr int64_t kGemmPartsReduceStages = 2;
 
 // A group of products with M > 16: one launch over one workgroup per CU,
 // the items' (tile, stage) iterations in stream-K order or, for many tiles,
@@ -897,6 +901,34 @@ static int32_t group_create_gemm(mnb_context *ctx, int32_t count, const mnb_grou
         for (int32_t g = 0; g < plan.G; ++g) m = std::max<int64_t>(m, r[(size_t)g + 1].iter - r[(size_t)g].iter);
         return m;
     };
+    // A tile longer than a workgroup's mean share of the stages sets the
+    // busiest workgroup of a tile list (Qwen2.5-0.5B's down tiles at M = 64:
+    // 38 stages against a mean of 31).  Where a tile's fp32 partial fits one
+    // workspace slot (all but 128 x 512 tiles), the tiles longer than the
+    // mean are cut along K into parts, summed by a reduce launch after the
+    // GEMM, when that shortens the busiest workgroup by more than the reduce
+    // costs; the parts' partial tiles must fit the context's workspace.
+    auto try_parts = [&]() {
+        plan.parts.n = 0;
+        if (seq.empty() || 32 * plan.fm * 128 * plan.ntw > mnb::kSkPartialFloats) return;
+        const int64_t mean = (plan.iters + plan.G - 1) / plan.G, b0 = busiest(wg);
+        if (b0 <= mean + kGemmPartsReduceStages) return;
+        std::vector<mnb::SkTile> seq_p;
+        std::vector<mnb::SkRange> wg_p;
+        if (!mnb::sk_tile_list_parts(plan.host, plan.G, mean, seq_p, wg_p, plan.parts)) {
+            plan.parts.n = 0;
+            return;
+        }
+        int n_parts = 0;
+        for (int j = 0; j < plan.parts.n; ++j) n_parts = std::max(n_parts, (int)plan.parts.e[j].last + 1);
+        if (plan.parts.n == 0 || n_parts > 2 * mnb::sk_max_grid(ctx->cu_count) ||
+            busiest(wg_p) + kGemmPartsReduceStages >= b0) {
+            plan.parts.n = 0;
+            return;
+        }
+        seq.swap(seq_p);
+        wg.swap(wg_p);
+    };
     // Rows of at most 32 (64) per item: 32-row (64-row) tiles of 512 columns
     // (128-row tiles would multiply by up to 8 (2) the MFMA work).
     int32_t max_m = 0;
@@ -913,13 +945,16 @@ static int32_t group_create_gemm(mnb_context *ctx, int32_t count, const mnb_grou
             narrow_iters += (int64_t)mnb::sk_tiles(items[i].M, g.NT, mnb::kGemmNTW, mnb::kGemmFM) * g.ST;
         }
         mnb::sk_tile_list(plan.host, plan.G, seq, wg);
+        try_parts();
         if ((double)busiest(wg) * kGemmHalfStageCost < (double)narrow_iters / plan.G) return true;
         seq.clear();
         wg.clear();
+        plan.parts.n = 0;
         return false;
     };
     if (max_m <= kGemmSkinnyMaxM && wide_ok && build(mnb::kGemmWideNTW, mnb::kGemmSkinnyFM) && tiles >= min_tiles) {
         mnb::sk_tile_list(plan.host, plan.G, seq, wg);
+        try_parts();
     } else if (max_m <= kGemmHalfMaxM && wide_ok && build(mnb::kGemmWideNTW, mnb::kGemmHalfFM) && tiles >= plan.G &&
                half_wins()) {
         // 64 x 512 tiles in tile-list order
@@ -943,6 +978,7 @@ static int32_t group_create_gemm(mnb_context *ctx, int32_t count, const mnb_grou
                 build(mnb::kGemmNTW);
             }
         }
+        if (plan.ntw == mnb::kGemmNTW) try_parts();
     }
     DeviceGuard guard(ctx->device);
     hipError_t e;
@@ -1117,7 +1153,7 @@ int32_t mnb_group_plan(const mnb_group *group, mnb_plan_info *out) {
     if (group->gemm) {
         const mnb::GemmGroupPlan &g = group->gplan;
         out->kernel = MNB_KERNEL_GEMM;
-        out->order = g.seq ? MNB_ORDER_TILE_LIST : MNB_ORDER_STREAM_K;
+        out->order = !g.seq ? MNB_ORDER_STREAM_K : g.parts.n > 0 ? MNB_ORDER_TILE_LIST_PARTS : MNB_ORDER_TILE_LIST;
         out->tile_rows = 32 * g.fm;
         out->tile_cols = 128 * g.ntw;
         out->workgroups = g.G;

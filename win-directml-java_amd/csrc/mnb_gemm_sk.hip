@@ -73,7 +73,6 @@ constexpr int kSkHalfFM = kGemmHalfFM;       // half-height tiles (tile-list lau
 constexpr int kSkStageRow = 80, kSkStageWave = 32 * kSkStageRow, kSkStageBytes = kSkWaves * kSkStageWave;
 constexpr int kSkThreads = 64 * kSkWaves;
 static_assert(kSkPartialFloats == kSkBM * kSkBN, "one fp32 partial tile, [kSkBM][kSkBN] row-major");
-constexpr int kSkReduceRows = 16;                 // rows of a partial tile per reduce workgroup
 constexpr int kSkReduceThreads = 256;             // each thread: 4 rows x 4 columns
 
 typedef float float16_t __attribute__((ext_vector_type(16)));
@@ -92,9 +91,10 @@ __device__ __forceinline__ float16_t mfma32x32x16(half8_t a, half8_t b, float16_
 // group order, tile t of an item covering m-tile t % MT and n-group t / MT,
 // and logical workgroup g owns iterations [g I / G, (g + 1) I / G).
 // Tile-list order (seq != nullptr): the tiles are listed in seq, workgroup
-// after workgroup, and logical workgroup g owns the whole tiles
-// seq[wg[g].pos ..] with iterations [wg[g].iter, wg[g + 1].iter), so no tile
-// is split.
+// after workgroup, and logical workgroup g owns the tiles seq[wg[g].pos ..]
+// with iterations [wg[g].iter, wg[g + 1].iter): whole tiles, or parts of a
+// tile cut along K (stages [st0, st0 + nst)), each written as the fp32
+// partial tile ws[part] for the reduce kernel.
 struct SkParams {
     SkItem one;             // the item when count == 1 (a single product)
     const SkItem *items;    // device table of count items (count > 1), ibeg ascending
@@ -104,7 +104,8 @@ struct SkParams {
     int32_t closed;         // 1: tile-list order of the single item `one` in closed form (sk_cf_*), no table
     int32_t G;              // workgroups
     int32_t I;              // iterations of all items (below 2^31)
-    float *ws;              // [G][2] partial tiles: slot 0 for a workgroup's first tile, 1 for its last
+    float *ws;              // partial tiles: stream-K [G][2] (slot 0 for a workgroup's first tile, 1 for its
+                            // last); tile list [part]
 };
 
 // Item i (uniform index).  The table is read through the constant address
@@ -140,6 +141,9 @@ __device__ __forceinline__ SkTile sk_seq(const SkParams &p, int i) {
     SkTile e;
     e.item = s[i].item;
     e.t = s[i].t;
+    e.st0 = s[i].st0;
+    e.nst = s[i].nst;
+    e.part = s[i].part;
     return e;
 }
 
@@ -159,15 +163,20 @@ __device__ __forceinline__ int sk_start(int g, const SkParams &p) {
 }
 
 // A cursor over the launch's tiles is item ci (fields ic), tile t of that
-// item and, in tile-list order, the list position pos (closed form: the
-// workgroup's own tile count so far, its tiles at block-order positions
-// cf_base + pos * cf_step).  Steps it to the next tile of the launch (the
-// caller knows there is one).
+// item, its stages [st0, end) and partial tile `part` (-1 for a whole tile
+// and in stream-K order, where the workgroup's range decides) and, in
+// tile-list order, the list position pos (closed form: the workgroup's own
+// tile count so far, its tiles at block-order positions cf_base + pos *
+// cf_step).  Steps it to the next tile of the launch (the caller knows there
+// is one).
 __device__ __forceinline__ void sk_next_tile(const SkParams &p, int &ci, int &t, int &pos, SkItem &ic, int cf_base,
-                                             int cf_step) {
+                                             int cf_step, int &st0, int &end, int &part) {
     if (p.closed) {
         ++pos;
         t = sk_cf_tile(ic.MT, ic.T / ic.MT, cf_base + pos * cf_step);
+        st0 = 0;
+        end = ic.ST;
+        part = -1;
     } else if (p.seq) {
         const SkTile e = sk_seq(p, ++pos);
         if (e.item != ci) {
@@ -175,18 +184,29 @@ __device__ __forceinline__ void sk_next_tile(const SkParams &p, int &ci, int &t,
             ic = sk_item(p, ci);
         }
         t = e.t;
-    } else if (++t == ic.T) {
-        t = 0;
-        ic = sk_item(p, ++ci);
+        st0 = e.st0;
+        end = e.st0 + e.nst;
+        part = e.part;
+    } else {
+        if (++t == ic.T) {
+            t = 0;
+            ic = sk_item(p, ++ci);
+        }
+        st0 = 0;
+        end = ic.ST;
+        part = -1;
     }
 }
 
-// k extent of the tile after the cursor's (the caller knows there is one).
-__device__ __forceinline__ int sk_next_kx(const SkParams &p, int ci, int t, int pos, const SkItem &ic) {
+// k extent and first stage of the tile after the cursor's (the caller knows
+// there is one).
+__device__ __forceinline__ int sk_next_kx(const SkParams &p, int ci, int t, int pos, const SkItem &ic, int &st0) {
+    st0 = 0;
     if (p.closed) return ic.kx;
     if (p.seq) {
-        const int item = sk_seq(p, pos + 1).item;
-        return item == ci ? ic.kx : sk_item(p, item).kx;
+        const SkTile e = sk_seq(p, pos + 1);
+        st0 = e.st0;
+        return e.item == ci ? ic.kx : sk_item(p, e.item).kx;
     }
     return t + 1 < ic.T ? ic.kx : sk_item(p, ci + 1).kx;
 }
@@ -291,9 +311,11 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     const int g = (p.G % 8 == 0) ? (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8) : (int)blockIdx.x;
     const int i0 = sk_start(g, p), i1 = sk_start(g + 1, p);
     if (i0 >= i1) return;
-    // compute cursor: the tile (item fields ic, tile t of the item) and the
-    // stage cst of the tile
-    int ci, t, cpos, cst;
+    // compute cursor: the tile (item fields ic, tile t of the item), the
+    // stage cst of the tile and the end cend of the tile's stages in this
+    // entry (the partial tile of a tile-list part is read from the list in
+    // the epilogue)
+    int ci, t, cpos, cst, cend = 0;
     const int cf_base = p.closed ? sk_cf_base(p.one.T, p.G, g) : 0, cf_step = sk_cf_step(p.G);
     if (p.closed) {
         cpos = 0;
@@ -305,7 +327,8 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
         const SkTile e = sk_seq(p, cpos);
         ci = e.item;
         t = e.t;
-        cst = 0;
+        cst = e.st0;
+        cend = e.st0 + e.nst;
     } else {
         cpos = 0;
         ci = sk_find_item(p, i0);
@@ -315,6 +338,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
         t = (i0 - ic.ibeg) / ic.ST;
         cst = (i0 - ic.ibeg) - t * ic.ST;
     }
+    if (!p.seq) cend = ic.ST;
 
     const uint32_t k6400 = vgpr_const(0x64006400u);
     const uint32_t ring0 = __builtin_amdgcn_readfirstlane(lds_addr(&ring[0][0]));
@@ -334,9 +358,9 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     constexpr int z_win_max = L::kZRegion - L::kWin;
     const int s_win = min(wave * NTW * L::kTileS, s_win_max);
     const int z_win = HAS_ZP ? min(wave * NTW * L::kTileZ, z_win_max) : 0;
-    // issue cursor: the tile (item fields iq, tile lt of the item), stage lst,
-    // iteration li
-    int ii = ci, lt = t, ipos = cpos, lst = cst, li = i0, lslot = 0;
+    // issue cursor: the tile (item fields iq, tile lt of the item), stage lst
+    // (of the entry's stages up to lend), iteration li
+    int ii = ci, lt = t, ipos = cpos, lst = cst, lend = cend, li = i0, lslot = 0;
     SkItem iq = ic;
     uint32_t xrow[L::kXDma], xcolk[L::kXDma], qoff[NTW], soff = 0, zoff = 0;
     auto set_tile = [&]() __attribute__((always_inline)) {
@@ -380,9 +404,9 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     auto advance = [&]() __attribute__((always_inline)) {
         if (li + 1 < i1) {
             ++li;
-            if (++lst == iq.ST) {
-                lst = 0;
-                sk_next_tile(p, ii, lt, ipos, iq, cf_base, cf_step);
+            if (++lst == lend) {
+                int lpart;
+                sk_next_tile(p, ii, lt, ipos, iq, cf_base, cf_step, lst, lend, lpart);
                 set_tile();
             }
         }
@@ -528,13 +552,13 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
                     }
                 }
             }
-        } else if constexpr (NTW == kSkNTW && FM == kSkFM) {
-            // partial tile of a split tile: [BM][kSkBN] fp32, summed by sk_reduce_kernel
-            // (wide, half and skinny tiles run in tile-list order only, where no tile is split);
-            // rows past M are neither stored nor summed
-            const int slot = first_seg ? 0 : 1;
+        } else if constexpr (BM * BN <= kSkPartialFloats) {
+            // partial tile of a split tile: [BM][BN] fp32, summed by sk_reduce_kernel
+            // (stream-K: this workgroup's slot; tile list: the entry's part; 128 x 512
+            // tiles are never split); rows past M are neither stored nor summed
+            const size_t pidx = p.seq ? (size_t)sk_seq(p, cpos).part : (size_t)g * 2 + (first_seg ? 0 : 1);
             __attribute__((address_space(1))) float *part =
-                (__attribute__((address_space(1))) float *)p.ws + ((size_t)g * 2 + slot) * kSkPartialFloats;
+                (__attribute__((address_space(1))) float *)p.ws + pidx * kSkPartialFloats;
 #pragma unroll
             for (int a = 0; a < FM; ++a)
                 if (m0 + a * 32 + c32 < ic.M) {
@@ -542,7 +566,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
                     for (int f = 0; f < FN; ++f)
 #pragma unroll
                         for (int j = 0; j < 4; ++j)
-                            *(__attribute__((address_space(1))) float4_t *)(part + (a * 32 + c32) * kSkBN + c_wave +
+                            *(__attribute__((address_space(1))) float4_t *)(part + (a * 32 + c32) * BN + c_wave +
                                                                              f * 32 + 8 * j + 4 * h) =
                                 (float4_t){acc[a][f][4 * j], acc[a][f][4 * j + 1], acc[a][f][4 * j + 2],
                                            acc[a][f][4 * j + 3]};
@@ -640,7 +664,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
         dequant(bf[0], 0);
     };
     int remaining = i1 - i0;
-    int seg_n = min(remaining, ic.ST - cst);  // stages of tile t done by this workgroup
+    int seg_n = min(remaining, cend - cst);   // stages of tile t done by this workgroup
     issue();                                   // stages 0 and 1 (three-slot ring: and 2)
     issue();
     land(0, cst, ic.kx);
@@ -680,7 +704,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             ++cst;
         } else {
             cst = 0;
-            if (remaining > seg_n) nkx = sk_next_kx(p, ci, t, cpos, ic);
+            if (remaining > seg_n) nkx = sk_next_kx(p, ci, t, cpos, ic, cst);
         }
         land(cslot, cst, nkx);
         // MFMAs of steps 6 and 7 with the DMA of a later stage between them,
@@ -713,8 +737,9 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             remaining -= seg_n;
             epilogue(seg_n);
             if (remaining == 0) break;
-            sk_next_tile(p, ci, t, cpos, ic, cf_base, cf_step);
-            seg_n = min(remaining, ic.ST);
+            int st0, part;   // st0 equals cst, set when this stage landed
+            sk_next_tile(p, ci, t, cpos, ic, cf_base, cf_step, st0, cend, part);
+            seg_n = min(remaining, cend - st0);
             kk = 0;
         }
     }
@@ -723,33 +748,41 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
 }
 
 // Sums the partial tiles of every split tile in contributor order and writes
-// y.  Workgroup (j, rb) reduces rows [rb * kSkReduceRows, +kSkReduceRows) of
-// split tile j of the list; each thread owns four rows of one 4-column group
+// y.  The tiles are BM x BN ([BM][BN] fp32 partial tiles); workgroup (j, rb)
+// reduces rows [rb * RB, +RB) of split tile j of the list (RB = 16 rows of
+// 256 columns or 8 of 512); each thread owns four rows of one 4-column group
 // and keeps the loads of up to kBatch contributors (4 kBatch 16-byte loads)
 // in flight before it adds them in contributor order.
+template <int BM, int BN>
 __global__ __launch_bounds__(kSkReduceThreads) void sk_reduce_kernel(SkParams p, SkSplitList list) {
-    constexpr int kRowBlocks = kSkBM / kSkReduceRows;
-    constexpr int kColGroups = kSkBN / 4;
-    constexpr int kRowsPerThread = kSkReduceRows * kColGroups / kSkReduceThreads;
+    constexpr int RB = kSkReduceThreads * 16 / BN;
+    constexpr int kRowBlocks = BM / RB;
+    constexpr int kColGroups = BN / 4;
+    constexpr int kRowsPerThread = RB * kColGroups / kSkReduceThreads;
     constexpr int kRowStep = kSkReduceThreads / kColGroups;
     constexpr int kBatch = 8;
+    static_assert(kRowsPerThread == 4 && BM % RB == 0 && BM * BN <= kSkPartialFloats, "reduce shape");
     const SkSplit e = list.e[blockIdx.x / kRowBlocks];
     const int rb = (int)blockIdx.x % kRowBlocks;
-    const int t = e.t_slot & 0x7fffffff;
-    const size_t slot0 = (uint32_t)e.t_slot >> 31;
+    const uint32_t flags = (uint32_t)e.t_slot;
+    const int t = (int)(flags & kSkSplitTile);
+    const bool parts = (flags & kSkSplitParts) != 0;
+    const size_t slot0 = (flags & kSkSplitSlot1) ? 1 : 0;
     const SkItem it = sk_item(p, e.item);
-    const int g_first = e.g_first, nc = (int)e.g_last - (int)e.g_first + 1;
+    const int first = e.first, nc = (int)e.last - (int)e.first + 1;
     const int tid = (int)threadIdx.x;
     const int c = (tid % kColGroups) * 4;
-    const int r0 = rb * kSkReduceRows + tid / kColGroups;
-    const int m0 = (t % it.MT) * kSkBM, n = (t / it.MT) * kSkBN + c;
+    const int r0 = rb * RB + tid / kColGroups;
+    const int m0 = (t % it.MT) * BM, n = (t / it.MT) * BN + c;
     // rows past M hold no partial sums (the GEMM does not store them): a
-    // workgroup whose 16 rows all lie past M has nothing to do; in the block
+    // workgroup whose rows all lie past M has nothing to do; in the block
     // that M cuts, the loads of rows past M read values that are never stored
-    if (n >= it.N || m0 + rb * kSkReduceRows >= it.M) return;
+    if (n >= it.N || m0 + rb * RB >= it.M) return;
     auto part = [&](int i, int k) __attribute__((always_inline)) {
-        const size_t pt = (size_t)(g_first + i) * 2 + (i == 0 ? slot0 : 0);
-        return gld((const float4_t *)(p.ws + pt * kSkPartialFloats + (size_t)(r0 + k * kRowStep) * kSkBN + c));
+        // tile list: the parts' partial tiles in K order; stream-K: the
+        // contributors' slots (the first one's slot0, the others' slot 0)
+        const size_t pt = parts ? (size_t)(first + i) : (size_t)(first + i) * 2 + (i == 0 ? slot0 : 0);
+        return gld((const float4_t *)(p.ws + pt * kSkPartialFloats + (size_t)(r0 + k * kRowStep) * BN + c));
     };
     float4_t sum[kRowsPerThread];
     for (int i0 = 0; i0 < nc; i0 += kBatch) {
@@ -771,6 +804,24 @@ __global__ __launch_bounds__(kSkReduceThreads) void sk_reduce_kernel(SkParams p,
         const int m = m0 + r0 + k * kRowStep;
         if (m < it.M) store_y4(it, m, n, sum[k]);
     }
+}
+
+// The reduce launch over `list` for tiles of 32 fm rows x 128 ntw columns.
+static hipError_t launch_reduce(int ntw, int fm, hipStream_t stream, const SkParams &p, const SkSplitList &list) {
+    if (list.n <= 0) return hipSuccess;
+    const int bm = 32 * fm, bn = 128 * ntw;
+    const int blocks = list.n * (bm / (kSkReduceThreads * 16 / bn));
+    if (bm == kSkBM && bn == kSkBN)
+        hipLaunchKernelGGL((sk_reduce_kernel<kSkBM, kSkBN>), dim3(blocks), dim3(kSkReduceThreads), 0, stream, p, list);
+    else if (bm == 32 * kSkHalfFM && bn == 128 * kSkWideNTW)
+        hipLaunchKernelGGL((sk_reduce_kernel<32 * kSkHalfFM, 128 * kSkWideNTW>), dim3(blocks), dim3(kSkReduceThreads), 0,
+                           stream, p, list);
+    else if (bm == 32 * kSkSkinnyFM && bn == 128 * kSkWideNTW)
+        hipLaunchKernelGGL((sk_reduce_kernel<32 * kSkSkinnyFM, 128 * kSkWideNTW>), dim3(blocks), dim3(kSkReduceThreads), 0,
+                           stream, p, list);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
 }
 
 SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg, int ntw, int fm) {
@@ -819,15 +870,27 @@ static void launch_sk_variant(int ntw, int fm, dim3 grid, dim3 block, hipStream_
 // inside a tile, the reduce kernel.  A stream-K launch needs ws_bytes of at
 // least sk_workspace_bytes(G); else nothing is launched.
 static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem *host, int32_t count,
-                            const SkTile *seq, const SkRange *wg, bool closed, int ntw, int fm, int64_t iters,
-                            int scale_f32, int has_zp, int sps, int G, float *ws, size_t ws_bytes, hipStream_t stream) {
+                            const SkTile *seq, const SkRange *wg, const SkSplitList *parts, bool closed, int ntw,
+                            int fm, int64_t iters, int scale_f32, int has_zp, int sps, int G, float *ws,
+                            size_t ws_bytes, hipStream_t stream) {
     if (iters >= (int64_t)1 << 31 || G < 1 || G > kSkMaxGrid) return hipErrorInvalidValue;
     if (closed && (count != 1 || seq)) return hipErrorInvalidValue;
+    if (parts && (!seq || parts->n < 0 || parts->n > kSkMaxSplits)) return hipErrorInvalidValue;
     // a stream-K launch may split tiles: the workspace must hold the partial
-    // tiles of its G workgroups
+    // tiles of its G workgroups; a tile list with parts, its parts' partials
     if (!seq && !closed && (!ws || ws_bytes < sk_workspace_bytes(G))) return hipErrorInvalidValue;
+    if (parts && parts->n > 0) {
+        int n_parts = 0;
+        for (int j = 0; j < parts->n; ++j) {
+            if (!((uint32_t)parts->e[j].t_slot & kSkSplitParts)) return hipErrorInvalidValue;
+            n_parts = std::max(n_parts, (int)parts->e[j].last + 1);
+        }
+        if (!ws || ws_bytes < (size_t)n_parts * kSkPartialFloats * sizeof(float) ||
+            32 * fm * 128 * ntw > kSkPartialFloats)
+            return hipErrorInvalidValue;
+    }
     // 256 x 128 tiles, or wide (512 x 128), half (512 x 64) and skinny (512 x 32) tiles in
-    // tile-list order only (no split tiles, no partial tiles)
+    // tile-list order only (split only into listed parts, never 512 x 128 tiles)
     const bool narrow = ntw == kSkNTW && fm == kSkFM;
     const bool wide = ntw == kSkWideNTW && (fm == kSkFM || fm == kSkHalfFM || fm == kSkSkinnyFM);
     if (!narrow && (!wide || !(seq || closed) || !sk_wide_supported(scale_f32, sps))) return hipErrorInvalidValue;
@@ -859,38 +922,33 @@ static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem
 #undef MNB_SK_SPS
 #undef MNB_SK_LAUNCH
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || seq || closed) return e;
-    // split tiles exist when some range boundary falls inside a tile (never
-    // in tile-list order)
+    if (e != hipSuccess || closed) return e;
+    if (seq) return parts ? launch_reduce(ntw, fm, stream, p, *parts) : hipSuccess;
+    // stream-K: split tiles exist when some range boundary falls inside a tile
     SkSplitList list;
     sk_split_list(host, count, iters, G, list);
-    if (list.n > 0) {
-        hipLaunchKernelGGL(sk_reduce_kernel, dim3(list.n * (kSkBM / kSkReduceRows)), dim3(kSkReduceThreads), 0, stream, p,
-                           list);
-        e = hipGetLastError();
-    }
-    return e;
+    return launch_reduce(ntw, fm, stream, p, list);
 }
 
 hipError_t launch_gemm_sk(const mnb_weight *w, const MatmulArgs &a, int G, float *ws, size_t ws_bytes,
                           hipStream_t stream) {
     const WeightGeom &g = w->g;
     const SkItem one = sk_make_item(w, a, 0);
-    return launch_sk(one, nullptr, &one, 1, nullptr, nullptr, false, kSkNTW, kSkFM, (int64_t)one.T * g.ST, g.scale_f32,
-                     g.has_zp, g.SPS, G, ws, ws_bytes, stream);
+    return launch_sk(one, nullptr, &one, 1, nullptr, nullptr, nullptr, false, kSkNTW, kSkFM, (int64_t)one.T * g.ST,
+                     g.scale_f32, g.has_zp, g.SPS, G, ws, ws_bytes, stream);
 }
 
 hipError_t launch_gemm_closed(const mnb_weight *w, const MatmulArgs &a, int ntw, int fm, int G, hipStream_t stream) {
     const WeightGeom &g = w->g;
     const SkItem one = sk_make_item(w, a, 0, ntw, fm);
-    return launch_sk(one, nullptr, &one, 1, nullptr, nullptr, true, ntw, fm, (int64_t)one.T * g.ST, g.scale_f32,
-                     g.has_zp, g.SPS, std::min(G, one.T), nullptr, 0, stream);
+    return launch_sk(one, nullptr, &one, 1, nullptr, nullptr, nullptr, true, ntw, fm, (int64_t)one.T * g.ST,
+                     g.scale_f32, g.has_zp, g.SPS, std::min(G, one.T), nullptr, 0, stream);
 }
 
 hipError_t launch_gemm_group(const GemmGroupPlan &g, float *ws, size_t ws_bytes, hipStream_t stream) {
     return launch_sk(g.host[0], (const SkItem *)g.items, g.host.data(), g.count, (const SkTile *)g.seq,
-                     (const SkRange *)g.wg, false, g.ntw, g.fm, g.iters, g.scale_f32, g.has_zp, g.sps, g.G, ws,
-                     ws_bytes, stream);
+                     (const SkRange *)g.wg, g.parts.n > 0 ? &g.parts : nullptr, false, g.ntw, g.fm, g.iters,
+                     g.scale_f32, g.has_zp, g.sps, g.G, ws, ws_bytes, stream);
 }
 
 }  // namespace mnb

@@ -233,6 +233,7 @@ struct GemmGroupPlan {
     int32_t fm = kGemmFM;           // 32-row fragments per tile (kGemmSkinnyFM: tile-list order, wide)
     int64_t iters = 0;
     int32_t scale_f32 = 0, has_zp = 0, sps = 0;
+    SkSplitList parts{};            // tile list with parts: the cut tiles, summed by the reduce launch (n = 0: none)
 };
 
 // Stream-K GEMM (M > 16): G persistent workgroups share the (tile, k-stage)

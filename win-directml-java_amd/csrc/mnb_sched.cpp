@@ -10,28 +10,49 @@
 
 namespace mnb {
 
-void sk_tile_list(const std::vector<SkItem> &items, int G, std::vector<SkTile> &seq, std::vector<SkRange> &wg) {
+bool sk_tile_list_parts(const std::vector<SkItem> &items, int G, int64_t split_above, std::vector<SkTile> &seq,
+                        std::vector<SkRange> &wg, SkSplitList &list) {
     constexpr int kBlock = 32;    // tiles of one block: what the workgroups of one XCD run side by side
     constexpr int kBlockM = 4;    // m-tiles per block (so 8 n-groups): the fewest x and weight bytes per stage
     constexpr int kTileCost = 2;  // epilogue of a tile, in stages (balance only)
+    list.n = 0;
+    int32_t parts = 0;
     // (1) the launch's tiles in block order: per item, chunks of kBlockM
     // m-tiles; per chunk, blocks of nb n-groups (consecutive blocks of a
-    // chunk share its x rows)
+    // chunk share its x rows); a tile longer than split_above stages as its
+    // parts, side by side
     std::vector<SkTile> order;
     for (int i = 0; i < (int)items.size(); ++i) {
         const SkItem &it = items[(size_t)i];
         const int MT = it.MT, NG = it.T / it.MT;
+        const int np = split_above > 0 && it.ST > split_above ? (int)((it.ST + split_above - 1) / split_above) : 1;
         for (int m0 = 0; m0 < MT; m0 += kBlockM) {
             const int m1 = std::min(MT, m0 + kBlockM), nb = kBlock / (m1 - m0);
             for (int n0 = 0; n0 < NG; n0 += nb)
                 for (int m = m0; m < m1; ++m)
-                    for (int n = n0; n < std::min(NG, n0 + nb); ++n) order.push_back(SkTile{i, m + n * MT});
+                    for (int n = n0; n < std::min(NG, n0 + nb); ++n) {
+                        const int t = m + n * MT;
+                        if (np == 1) {
+                            order.push_back(SkTile{i, t, 0, it.ST, -1});
+                            continue;
+                        }
+                        if (list.n == kSkMaxSplits || parts + np > kSkMaxParts) return false;
+                        SkSplit &e = list.e[list.n++];
+                        e.t_slot = (int32_t)((uint32_t)t | kSkSplitParts);
+                        e.item = (uint16_t)i;
+                        e.first = (uint8_t)parts;
+                        e.last = (uint8_t)(parts + np - 1);
+                        for (int j = 0; j < np; ++j) {
+                            const int s0 = (int)((int64_t)j * it.ST / np), s1 = (int)((int64_t)(j + 1) * it.ST / np);
+                            order.push_back(SkTile{i, t, s0, s1 - s0, parts++});
+                        }
+                    }
         }
     }
     // (2) one contiguous chunk of equal cost per XCD
     const int X = G % 8 == 0 ? 8 : 1, per = G / X;
     int64_t total = 0;
-    for (const SkTile &e : order) total += items[(size_t)e.item].ST + kTileCost;
+    for (const SkTile &e : order) total += e.nst + kTileCost;
     // (3) each chunk dealt to its XCD's workgroups, least loaded first, its
     // longest tiles first (a stable order, so each item's tiles keep their
     // block order and still run side by side; longest first keeps the
@@ -39,7 +60,7 @@ void sk_tile_list(const std::vector<SkItem> &items, int G, std::vector<SkTile> &
     std::vector<std::vector<SkTile>> chunks((size_t)X);
     int64_t before = 0;
     for (const SkTile &e : order) {
-        const int64_t c = items[(size_t)e.item].ST + kTileCost;
+        const int64_t c = e.nst + kTileCost;
         const int x = (int)std::min<int64_t>(X - 1, (2 * before + c) * X / (2 * total));
         before += c;
         chunks[(size_t)x].push_back(e);
@@ -48,11 +69,9 @@ void sk_tile_list(const std::vector<SkItem> &items, int G, std::vector<SkTile> &
     std::vector<int64_t> load((size_t)G, 0);
     for (int x = 0; x < X; ++x) {
         std::vector<SkTile> &ch = chunks[(size_t)x];
-        std::stable_sort(ch.begin(), ch.end(), [&](const SkTile &a, const SkTile &b) {
-            return items[(size_t)a.item].ST > items[(size_t)b.item].ST;
-        });
+        std::stable_sort(ch.begin(), ch.end(), [](const SkTile &a, const SkTile &b) { return a.nst > b.nst; });
         for (const SkTile &e : ch) {
-            const int64_t c = items[(size_t)e.item].ST + kTileCost;
+            const int64_t c = e.nst + kTileCost;
             int best = x * per;
             for (int w = x * per + 1; w < (x + 1) * per; ++w)
                 if (load[(size_t)w] < load[(size_t)best]) best = w;
@@ -68,10 +87,16 @@ void sk_tile_list(const std::vector<SkItem> &items, int G, std::vector<SkTile> &
         wg[(size_t)g] = SkRange{(int32_t)seq.size(), (int32_t)iter};
         for (const SkTile &e : lists[(size_t)g]) {
             seq.push_back(e);
-            iter += items[(size_t)e.item].ST;
+            iter += e.nst;
         }
     }
     wg[(size_t)G] = SkRange{(int32_t)seq.size(), (int32_t)iter};
+    return true;
+}
+
+void sk_tile_list(const std::vector<SkItem> &items, int G, std::vector<SkTile> &seq, std::vector<SkRange> &wg) {
+    SkSplitList none;
+    sk_tile_list_parts(items, G, 0, seq, wg, none);
 }
 
 bool stream_schedule(const std::vector<int32_t> &NT, const std::vector<int32_t> &ST, int64_t waves,
@@ -209,10 +234,10 @@ void sk_split_list(const SkItem *host, int32_t count, int64_t iters, int G, SkSp
         int64_t g_last = b;                              // the owner of the tile's last iteration
         while (g_last + 1 < G && start(g_last + 1) <= ts + it.ST - 1) ++g_last;
         SkSplit &e = list.e[list.n++];
-        e.t_slot = (int32_t)((uint32_t)t | (start(b - 1) == ts ? 0u : 0x80000000u));
+        e.t_slot = (int32_t)((uint32_t)t | (start(b - 1) == ts ? 0u : kSkSplitSlot1));
         e.item = (uint16_t)k;
-        e.g_first = (uint8_t)(b - 1);
-        e.g_last = (uint8_t)g_last;
+        e.first = (uint8_t)(b - 1);
+        e.last = (uint8_t)g_last;
     }
 }
 

@@ -32,10 +32,14 @@ struct SkItem {
 };
 
 // Tile-list order of a GEMM launch: tile t of item `item` (m-tile t % MT,
-// n-group t / MT), and the start of one workgroup's tiles (list position,
-// first iteration).
+// n-group t / MT), its stages [st0, st0 + nst) (a whole tile: 0 and ST) and,
+// for a part of a tile cut along K, the index of the fp32 partial tile it
+// writes into the workspace (-1: a whole tile, which writes y); and the start
+// of one workgroup's tiles (list position, first iteration).
 struct SkTile {
     int32_t item, t;
+    int32_t st0 = 0, nst = 0;
+    int32_t part = -1;
 };
 struct SkRange {
     int32_t pos, iter;
@@ -154,17 +158,23 @@ struct SinglePlan {
 };
 SinglePlan sk_single_plan(int M, int NT, int ST, int scale_f32, int sps, int cu_count);
 
-// The split tiles of one stream-K launch (the ranges of G logical
-// workgroups over `iters` iterations, range g = [g iters / G, (g + 1) iters /
-// G)), listed by the host at launch time and passed by value in the reduce
-// kernel's arguments, so nothing is allocated: tile t of item `item`, its
-// contributors g_first .. g_last (the workgroups whose ranges hold some of
-// its stages, in that order); g_first's partial tile is in its slot 0 when
-// the tile starts its range, else slot 1; the others' are in their slot 0.
+// The split tiles of one launch, passed by value in the reduce kernel's
+// arguments, so nothing is allocated: tile t of item `item` and its
+// contributors first .. last in K order.
+// - Stream-K (the ranges of G logical workgroups over `iters` iterations,
+//   range g = [g iters / G, (g + 1) iters / G), listed by the host at launch
+//   time): first .. last are the workgroups whose ranges hold some of the
+//   tile's stages; first's partial tile is in its slot 0 when the tile starts
+//   its range, else slot 1 (bit 31); the others' are in their slot 0.
+// - Tile list with parts (bit 30): first .. last are the indices of the
+//   parts' partial tiles.
+// t < 2^30: a split tile has at least two stages and a launch fewer than
+// 2^31 iterations.
+constexpr uint32_t kSkSplitSlot1 = 0x80000000u, kSkSplitParts = 0x40000000u, kSkSplitTile = 0x3fffffffu;
 struct SkSplit {
-    int32_t t_slot;     // t | (slot of g_first's partial tile << 31)
+    int32_t t_slot;     // t | kSkSplitSlot1 | kSkSplitParts
     uint16_t item;
-    uint8_t g_first, g_last;
+    uint8_t first, last;
 };
 constexpr int kSkMaxSplits = kSkMaxGrid - 1;   // at most one split tile per range boundary
 struct SkSplitList {
@@ -174,6 +184,20 @@ struct SkSplitList {
 // Fills `list` for items host[0 .. count) (ibeg ascending, iters in all,
 // G <= kSkMaxGrid): each split tile once, at the first range boundary inside it.
 void sk_split_list(const SkItem *host, int32_t count, int64_t iters, int G, SkSplitList &list);
+
+// A tile list whose tiles of more than split_above stages are cut along K
+// into ceil(ST / split_above) parts of equal stages (to within one), so that
+// one long tile no longer sets the busiest workgroup.  The parts of a tile
+// are listed side by side in block order and dealt like tiles; each writes
+// an fp32 partial tile (workspace index `part`, numbered tile by tile), and
+// `list` names every cut tile with its parts first .. last (tile-list flag
+// set), for the reduce kernel to sum in K order.  Returns false when the
+// parts would need more than kSkMaxParts partial tiles or kSkMaxSplits cut
+// tiles (seq, wg and list are then unspecified).  split_above <= 0 cuts
+// nothing (sk_tile_list).
+constexpr int kSkMaxParts = 256;
+bool sk_tile_list_parts(const std::vector<SkItem> &items, int G, int64_t split_above, std::vector<SkTile> &seq,
+                        std::vector<SkRange> &wg, SkSplitList &list);
 
 // The streaming kernel's unit of issue: up to kStreamJobTiles consecutive
 // super-tiles of one n-tile (a unit of ST super-tiles is stream_jobs(ST)

@@ -96,7 +96,7 @@ class TripletInfo(ctypes.Structure):
 
 
 MNB_KERNEL_GEMV, MNB_KERNEL_STREAM, MNB_KERNEL_GEMV_GROUP, MNB_KERNEL_GEMM, MNB_KERNEL_KSLICE = 1, 2, 3, 4, 5
-MNB_ORDER_NONE, MNB_ORDER_STREAM_K, MNB_ORDER_TILE_LIST = 0, 1, 2
+MNB_ORDER_NONE, MNB_ORDER_STREAM_K, MNB_ORDER_TILE_LIST, MNB_ORDER_TILE_LIST_PARTS = 0, 1, 2, 3
 
 
 class PlanInfo(ctypes.Structure):
