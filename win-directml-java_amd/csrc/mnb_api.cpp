@@ -832,10 +832,13 @@ constexpr int kGemmSkinnyMaxM = 32, kGemmHalfMaxM = 64;
 // Cost of a 64 x 512 stage in 128 x 256 stages: the same MFMA work and the
 // same operand bytes (x and weights trade places), rounded up.
 constexpr double kGemmHalfStageCost = 1.1;
-// Cost of the reduce launch after a tile list with parts, in stages of the
-// busiest workgroup (a launch and the partial tiles read back: ~4 us against
-// ~2.5 us per 64 x 512 stage).
-constexpr int64_t kGemmPartsReduceStages = 2;
+// Cost of cutting a tile list into parts, in stages of the busiest
+// workgroup: the reduce launch (~5 us against ~2.5 us per 64 x 512 stage) and
+// the fp32 partial tiles written and read back.  The Qwen2.5-0.5B step at
+// M = 64, whose parts take its busiest workgroup from 38 to 35 stages, ran
+// 1-3% slower with them on two boxes and 2% faster on a third, so a cut must
+// save more than 4 stages.
+constexpr int64_t kGemmPartsReduceStages = 4;
 
 // A group of products with M > 16: one launch over one workgroup per CU,
 // the items' (tile, stage) iterations in stream-K order or, for many tiles,

@@ -164,11 +164,12 @@ __device__ __forceinline__ int sk_start(int g, const SkParams &p) {
 
 // A cursor over the launch's tiles is item ci (fields ic), tile t of that
 // item, its stages [st0, end) and partial tile `part` (-1 for a whole tile
-// and in stream-K order, where the workgroup's range decides) and, in
-// tile-list order, the list position pos (closed form: the workgroup's own
-// tile count so far, its tiles at block-order positions cf_base + pos *
-// cf_step).  Steps it to the next tile of the launch (the caller knows there
-// is one).
+// and in stream-K order, where the workgroup's range decides; a tile list
+// has parts only in the PARTS kernels) and, in tile-list order, the list
+// position pos (closed form: the workgroup's own tile count so far, its
+// tiles at block-order positions cf_base + pos * cf_step).  Steps it to the
+// next tile of the launch (the caller knows there is one).
+template <bool PARTS>
 __device__ __forceinline__ void sk_next_tile(const SkParams &p, int &ci, int &t, int &pos, SkItem &ic, int cf_base,
                                              int cf_step, int &st0, int &end, int &part) {
     if (p.closed) {
@@ -184,9 +185,15 @@ __device__ __forceinline__ void sk_next_tile(const SkParams &p, int &ci, int &t,
             ic = sk_item(p, ci);
         }
         t = e.t;
-        st0 = e.st0;
-        end = e.st0 + e.nst;
-        part = e.part;
+        if constexpr (PARTS) {
+            st0 = e.st0;
+            end = e.st0 + e.nst;
+            part = e.part;
+        } else {
+            st0 = 0;
+            end = ic.ST;
+            part = -1;
+        }
     } else {
         if (++t == ic.T) {
             t = 0;
@@ -200,12 +207,13 @@ __device__ __forceinline__ void sk_next_tile(const SkParams &p, int &ci, int &t,
 
 // k extent and first stage of the tile after the cursor's (the caller knows
 // there is one).
+template <bool PARTS>
 __device__ __forceinline__ int sk_next_kx(const SkParams &p, int ci, int t, int pos, const SkItem &ic, int &st0) {
     st0 = 0;
     if (p.closed) return ic.kx;
     if (p.seq) {
         const SkTile e = sk_seq(p, pos + 1);
-        st0 = e.st0;
+        if constexpr (PARTS) st0 = e.st0;
         return e.item == ci ? ic.kx : sk_item(p, e.item).kx;
     }
     return t + 1 < ic.T ? ic.kx : sk_item(p, ci + 1).kx;
@@ -288,7 +296,10 @@ struct SkSlot {
     static_assert(NTW * kTileS <= kWin && NTW * kTileZ <= kWin, "a wave's scales fit one window");
 };
 
-template <typename ScaleT, bool HAS_ZP, int SPS, int NTW, int FM>
+// PARTS: a tile list with parts (tiles cut along K, written as partial
+// tiles); the other launches (stream-K, closed form, whole-tile lists) run
+// the kernel without the parts' bookkeeping.
+template <typename ScaleT, bool HAS_ZP, int SPS, int NTW, int FM, bool PARTS>
 __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     using L = SkSlot<ScaleT, HAS_ZP, SPS, NTW, FM>;
     constexpr int BM = L::BM;                        // rows per tile (128, 64, or 32 for skinny tiles)
@@ -327,7 +338,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
         const SkTile e = sk_seq(p, cpos);
         ci = e.item;
         t = e.t;
-        cst = e.st0;
+        cst = PARTS ? e.st0 : 0;
         cend = e.st0 + e.nst;
     } else {
         cpos = 0;
@@ -338,7 +349,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
         t = (i0 - ic.ibeg) / ic.ST;
         cst = (i0 - ic.ibeg) - t * ic.ST;
     }
-    if (!p.seq) cend = ic.ST;
+    if (!PARTS || !p.seq) cend = ic.ST;
 
     const uint32_t k6400 = vgpr_const(0x64006400u);
     const uint32_t ring0 = __builtin_amdgcn_readfirstlane(lds_addr(&ring[0][0]));
@@ -404,9 +415,9 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     auto advance = [&]() __attribute__((always_inline)) {
         if (li + 1 < i1) {
             ++li;
-            if (++lst == lend) {
+            if (++lst == (PARTS ? lend : iq.ST)) {
                 int lpart;
-                sk_next_tile(p, ii, lt, ipos, iq, cf_base, cf_step, lst, lend, lpart);
+                sk_next_tile<PARTS>(p, ii, lt, ipos, iq, cf_base, cf_step, lst, lend, lpart);
                 set_tile();
             }
         }
@@ -552,11 +563,11 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
                     }
                 }
             }
-        } else if constexpr (BM * BN <= kSkPartialFloats) {
+        } else if constexpr (PARTS ? BM * BN <= kSkPartialFloats : NTW == kSkNTW && FM == kSkFM) {
             // partial tile of a split tile: [BM][BN] fp32, summed by sk_reduce_kernel
-            // (stream-K: this workgroup's slot; tile list: the entry's part; 128 x 512
-            // tiles are never split); rows past M are neither stored nor summed
-            const size_t pidx = p.seq ? (size_t)sk_seq(p, cpos).part : (size_t)g * 2 + (first_seg ? 0 : 1);
+            // (stream-K, 128 x 256 tiles only: this workgroup's slot; a tile list with
+            // parts: the entry's part); rows past M are neither stored nor summed
+            const size_t pidx = PARTS ? (size_t)sk_seq(p, cpos).part : (size_t)g * 2 + (first_seg ? 0 : 1);
             __attribute__((address_space(1))) float *part =
                 (__attribute__((address_space(1))) float *)p.ws + pidx * kSkPartialFloats;
 #pragma unroll
@@ -704,7 +715,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             ++cst;
         } else {
             cst = 0;
-            if (remaining > seg_n) nkx = sk_next_kx(p, ci, t, cpos, ic, cst);
+            if (remaining > seg_n) nkx = sk_next_kx<PARTS>(p, ci, t, cpos, ic, cst);
         }
         land(cslot, cst, nkx);
         // MFMAs of steps 6 and 7 with the DMA of a later stage between them,
@@ -738,7 +749,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             epilogue(seg_n);
             if (remaining == 0) break;
             int st0, part;   // st0 equals cst, set when this stage landed
-            sk_next_tile(p, ci, t, cpos, ic, cf_base, cf_step, st0, cend, part);
+            sk_next_tile<PARTS>(p, ci, t, cpos, ic, cf_base, cf_step, st0, cend, part);
             seg_n = min(remaining, cend - st0);
             kk = 0;
         }
@@ -850,18 +861,26 @@ SkItem sk_make_item(const mnb_weight *w, const MatmulArgs &a, int32_t ibeg, int 
 
 // The kernel of one weight variant at tile width ntw and height 32 fm (wide
 // and skinny tiles exist for the variants whose four n-tiles of scales fit
-// one 1 KiB window).
+// one 1 KiB window), with or without parts (never for 128 x 512 tiles).
+template <typename ScaleT, bool HAS_ZP, int SPS, int NTW, int FM>
+static void launch_sk_parts(bool parts, dim3 grid, dim3 block, hipStream_t stream, const SkParams &p) {
+    if (parts)
+        hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, NTW, FM, true>), grid, block, 0, stream, p);
+    else
+        hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, NTW, FM, false>), grid, block, 0, stream, p);
+}
 template <typename ScaleT, bool HAS_ZP, int SPS>
-static void launch_sk_variant(int ntw, int fm, dim3 grid, dim3 block, hipStream_t stream, const SkParams &p) {
+static void launch_sk_variant(int ntw, int fm, bool parts, dim3 grid, dim3 block, hipStream_t stream,
+                              const SkParams &p) {
     if (ntw == kSkNTW) {
-        hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, kSkNTW, kSkFM>), grid, block, 0, stream, p);
+        launch_sk_parts<ScaleT, HAS_ZP, SPS, kSkNTW, kSkFM>(parts, grid, block, stream, p);
     } else if constexpr (kSkWideNTW * kTileRows * SPS * sizeof(ScaleT) <= 1024) {
         if (fm == kSkFM)
-            hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, kSkWideNTW, kSkFM>), grid, block, 0, stream, p);
+            hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, kSkWideNTW, kSkFM, false>), grid, block, 0, stream, p);
         else if (fm == kSkHalfFM)
-            hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, kSkWideNTW, kSkHalfFM>), grid, block, 0, stream, p);
+            launch_sk_parts<ScaleT, HAS_ZP, SPS, kSkWideNTW, kSkHalfFM>(parts, grid, block, stream, p);
         else
-            hipLaunchKernelGGL((gemm_sk_kernel<ScaleT, HAS_ZP, SPS, kSkWideNTW, kSkSkinnyFM>), grid, block, 0, stream, p);
+            launch_sk_parts<ScaleT, HAS_ZP, SPS, kSkWideNTW, kSkSkinnyFM>(parts, grid, block, stream, p);
     }
 }
 
@@ -905,7 +924,8 @@ static hipError_t launch_sk(const SkItem &one, const SkItem *items, const SkItem
     p.I = (int32_t)iters;
     p.ws = ws;
     dim3 grid(G), block(kSkThreads);
-#define MNB_SK_LAUNCH(ST_, ZP_, SPS_) launch_sk_variant<ST_, ZP_, SPS_>(ntw, fm, grid, block, stream, p)
+    const bool with_parts = parts && parts->n > 0;
+#define MNB_SK_LAUNCH(ST_, ZP_, SPS_) launch_sk_variant<ST_, ZP_, SPS_>(ntw, fm, with_parts, grid, block, stream, p)
 #define MNB_SK_SPS(ST_, ZP_)                           \
     switch (sps) {                                     \
         case 1: MNB_SK_LAUNCH(ST_, ZP_, 1); break;     \
