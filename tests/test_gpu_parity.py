@@ -676,6 +676,30 @@ def test_random_prefill_groups(ctx, seed):
         w.close()
 
 
+@pytest.mark.parametrize("rows", [32, 64, 128])
+@pytest.mark.parametrize("seed", [0, 1])
+def test_random_groups_with_parts(ctx, rows, seed):
+    """Random tile-list groups whose long items (K 4096 to 8192: 32 to 64
+    stages) are cut into parts among many short tiles (K up to 512): M up to
+    32, 33 to 64 or 65 to 600 (32 x 512, 64 x 512 or 128 x 256 tiles), N and
+    M tails, fp16 or fp32 y; every item against the oracle and its own single
+    launch, replays bitwise equal."""
+    rng = np.random.default_rng(9100 + 10 * seed + rows)
+    lo, hi = {32: (17, 32), 64: (33, 64), 128: (65, 600)}[rows]
+    bn = 256 if rows == 128 else 512
+    specs, tiles = [], 0
+    while tiles < 1100:
+        M, K, N = int(rng.integers(lo, hi + 1)), 8 * int(rng.integers(8, 65)), int(rng.integers(1000, 40001))
+        specs.append((M, K, N, [np.float16, np.float32][int(rng.integers(0, 2))], False))
+        tiles += ((M + rows - 1) // rows) * ((N + bn - 1) // bn)
+    for _ in range(int(rng.integers(1, 4))):
+        M, K, N = int(rng.integers(lo, hi + 1)), 8 * int(rng.integers(512, 1025)), int(rng.integers(256, 3001))
+        specs.append((M, K, N, [np.float16, np.float32][int(rng.integers(0, 2))], False))
+    say("random parts group", rows, seed, [sp[:3] for sp in specs])
+    for w, _, _ in _check_prefill_group(ctx, specs, 9200 + 10 * seed + rows, plan=(GEMM, PARTS, rows, bn)):
+        w.close()
+
+
 @pytest.mark.parametrize("cls", ["m1", "rows2to4", "rows5to16"])
 @pytest.mark.parametrize("seed", [0, 1])
 def test_random_small_groups(ctx, cls, seed):

@@ -907,30 +907,41 @@ static int32_t group_create_gemm(mnb_context *ctx, int32_t count, const mnb_grou
     // A tile longer than a workgroup's mean share of the stages sets the
     // busiest workgroup of a tile list (Qwen2.5-0.5B's down tiles at M = 64:
     // 38 stages against a mean of 31).  Where a tile's fp32 partial fits one
-    // workspace slot (all but 128 x 512 tiles), the tiles longer than the
-    // mean are cut along K into parts, summed by a reduce launch after the
-    // GEMM, when that shortens the busiest workgroup by more than the reduce
-    // costs; the parts' partial tiles must fit the context's workspace.
+    // workspace slot (all but 128 x 512 tiles), the long tiles are cut along
+    // K into parts, summed by a reduce launch after the GEMM, when that
+    // shortens the busiest workgroup by more than the reduce costs; the
+    // parts' partial tiles must fit the context's workspace.
+    // Parts of about the mean, a half, a third or a quarter of it are
+    // tried (parts near the mean pack unevenly: two of them on one
+    // workgroup double it), and the cut whose busiest workgroup finishes
+    // first is kept.
     auto try_parts = [&]() {
         plan.parts.n = 0;
         if (seq.empty() || 32 * plan.fm * 128 * plan.ntw > mnb::kSkPartialFloats) return;
         const int64_t mean = (plan.iters + plan.G - 1) / plan.G, b0 = busiest(wg);
         if (b0 <= mean + kGemmPartsReduceStages) return;
-        std::vector<mnb::SkTile> seq_p;
-        std::vector<mnb::SkRange> wg_p;
-        if (!mnb::sk_tile_list_parts(plan.host, plan.G, mean, seq_p, wg_p, plan.parts)) {
-            plan.parts.n = 0;
-            return;
+        int64_t best = b0 - kGemmPartsReduceStages;
+        std::vector<mnb::SkTile> seq_p, seq_best;
+        std::vector<mnb::SkRange> wg_p, wg_best;
+        mnb::SkSplitList parts;
+        for (int d = 1; d <= 4; ++d) {
+            const int64_t split = (mean + d - 1) / d;
+            if (split < 1 || !mnb::sk_tile_list_parts(plan.host, plan.G, split, seq_p, wg_p, parts) || parts.n == 0)
+                continue;
+            int n_parts = 0;
+            for (int j = 0; j < parts.n; ++j) n_parts = std::max(n_parts, (int)parts.e[j].last + 1);
+            if (n_parts > 2 * mnb::sk_max_grid(ctx->cu_count)) continue;
+            const int64_t b = busiest(wg_p);
+            if (b < best) {
+                best = b;
+                seq_best.swap(seq_p);
+                wg_best.swap(wg_p);
+                plan.parts = parts;
+            }
         }
-        int n_parts = 0;
-        for (int j = 0; j < plan.parts.n; ++j) n_parts = std::max(n_parts, (int)plan.parts.e[j].last + 1);
-        if (plan.parts.n == 0 || n_parts > 2 * mnb::sk_max_grid(ctx->cu_count) ||
-            busiest(wg_p) + kGemmPartsReduceStages >= b0) {
-            plan.parts.n = 0;
-            return;
-        }
-        seq.swap(seq_p);
-        wg.swap(wg_p);
+        if (plan.parts.n == 0) return;
+        seq.swap(seq_best);
+        wg.swap(wg_best);
     };
     // Rows of at most 32 (64) per item: 32-row (64-row) tiles of 512 columns
     // (128-row tiles would multiply by up to 8 (2) the MFMA work).
