@@ -598,11 +598,11 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     // the MFMA registers across stages.  A stage is: the head (DMA issue of
     // stage + 2, the stage's raw weights, scales and zero points, step 0's x
     // fragments and dequant), steps 0..5 (MFMAs of step s while step s + 1's
-    // operands are read and dequantized), the operands of steps 6 and 7 read
-    // into registers, the barrier that lands the next stage, and then the
-    // MFMAs of steps 6 and 7 issued together with the next stage's head, so
-    // the matrix core keeps running through the barrier while the DMA issue
-    // and the next stage's LDS reads are in flight.  Nothing reads a slot
+    // operands are read and dequantized), step 7's x fragments read into
+    // registers, the barrier that lands the next stage, and then the MFMAs
+    // of steps 6 and 7 issued together with the DMAs of a later stage and
+    // step 7's dequantization, before the next stage's head, so the matrix
+    // core keeps running through the barrier.  Nothing reads a slot
     // after the barrier that follows its last stage, so the DMA that the next
     // head issues into it is safe.
     //
@@ -668,7 +668,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
     int cslot = 0;                           // ring slot of the stage being computed
     constexpr int kSteps = kTileK / 16;      // 8 MFMA k-steps per stage
     half8_t af[2][FM], bf[2][FN];      // steps 0..6, alternating
-    half8_t af7[FM], bf7[FN];          // step 7, held across the barrier
+    half8_t af7[FM], bf7[FN];          // step 7: x read before the barrier, weights dequantized in the tail
     auto head_reads = [&]() __attribute__((always_inline)) {
         load_stage(cslot);
         read_x(af[0], cslot, 0);
@@ -709,8 +709,7 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             __builtin_amdgcn_sched_barrier(0);
         }
         // af[0], bf[0] hold step 6; step 7 goes to its own registers
-        read_x(af7, cslot, kSteps - 1);
-        dequant(bf7, kSteps - 1);
+        read_x(af7, cslot, kSteps - 1);   // step 7's weights are dequantized in the tail
         cslot = cslot == D - 1 ? 0 : cslot + 1;
         // the stage to land: the next of this segment, else the first of the
         // next tile (of this item or the next); after the last stage of the
@@ -731,18 +730,32 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             // the wave that has passed the barrier issues these first: the
             // SIMD's other wave is still in its own tail or stage (+0.7%)
             __builtin_amdgcn_s_setprio(1);
-            // one DMA after each tail MFMA (skinny tiles: the DMA left over
-            // after the last MFMA follows it)
+            // the DMAs spread over the tail MFMAs: after every second one
+            // for 128 x 512 tiles, after every one for the others (those
+            // left after the last MFMA follow it); step 7's dequantization
+            // after the fourth step-6 MFMA (the last one for skinny tiles),
+            // where the matrix core hides it (same box: +1.7% on the M=512
+            // group, +1-2% on the M <= 64 groups against issuing it before
+            // the barrier with one DMA per MFMA)
             constexpr int kTailMfma = 2 * FM * FN, kTailDma = L::kXDma + NTW + 1;
+            constexpr int kDmaGap = (FM == kSkFM && NTW == kSkWideNTW) ? 2 : 1;
+            constexpr int kDq7 = FM * FN - 1 < 3 ? FM * FN - 1 : 3;
+            auto dma_j = [&](int j) __attribute__((always_inline)) {
+                if (j < L::kXDma) dma_x(base, j);
+                else if (j < L::kXDma + NTW) dma_q(base, j - L::kXDma);
+                else dma_sz(base);
+            };
 #pragma unroll
-            for (int i = 0; i < (kTailMfma > kTailDma ? kTailMfma : kTailDma); ++i) {
+            for (int i = 0; i < kTailMfma; ++i) {
                 const int a = (i / FN) % FM, f = i % FN;
                 if (i < FM * FN) acc[a][f] = mfma32x32x16(bf[0][f], af[0][a], acc[a][f]);
-                else if (i < kTailMfma) acc[a][f] = mfma32x32x16(bf7[f], af7[a], acc[a][f]);
+                else acc[a][f] = mfma32x32x16(bf7[f], af7[a], acc[a][f]);
                 __builtin_amdgcn_sched_barrier(0);
-                if (i < L::kXDma) dma_x(base, i);
-                else if (i < L::kXDma + NTW) dma_q(base, i - L::kXDma);
-                else if (i == L::kXDma + NTW) dma_sz(base);
+#pragma unroll
+                for (int j = 0; j < kTailDma; ++j)
+                    if ((kDmaGap * j < kTailMfma ? kDmaGap * j : kTailMfma - 1) == i) dma_j(j);
+                __builtin_amdgcn_sched_barrier(0);
+                if (i == kDq7) dequant(bf7, kSteps - 1);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
