@@ -691,10 +691,13 @@ __global__ __launch_bounds__(kSkThreads, 1) void gemm_sk_kernel(SkParams p) {
             // order within the step: the next step's dequant VALU fills the
             // shadow of the first MFMAs, and the next step's x reads go out
             // between the last FM MFMAs (same box, M=512 group: +2.4% over
-            // issuing the x reads first; 5 + 2 VALU per MFMA for 128 x 512
-            // tiles, 4 + 3 for the others, whose 32-row groups lose with 5 + 2)
-            constexpr int kVa = (FM == kSkFM && NTW == kSkWideNTW) ? 5 : 4;
-            constexpr int kVb = (FM == kSkFM && NTW == kSkWideNTW) ? 2 : 3;
+            // issuing the x reads first).  VALU per MFMA: 5 + 2 for 128 x 512
+            // tiles; 7 + 6 for 64 x 512 tiles, which place all 26 of a step
+            // (+1.2% on the M=64 groups over 4 + 3); 4 + 3 for the others
+            // (32-row groups lose with 5 + 2 or with all 26 placed)
+            constexpr bool kWide128 = FM == kSkFM && NTW == kSkWideNTW, kWide64 = FM == kSkHalfFM && NTW == kSkWideNTW;
+            constexpr int kVa = kWide128 ? 5 : kWide64 ? 7 : 4;
+            constexpr int kVb = kWide128 ? 2 : kWide64 ? 6 : 3;
 #pragma unroll
             for (int i = 0; i < FM * FN - FM; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);     // MFMA
