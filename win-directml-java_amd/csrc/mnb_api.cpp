@@ -894,7 +894,7 @@ static int32_t group_create_gemm(mnb_context *ctx, int32_t count, const mnb_grou
     // fewer tiles keep the stream-K split, which balances any tile count.
     // The width is the one whose busiest workgroup finishes first: a
     // 512-column stage has twice the flops of a 256-column one and costs
-    // kGemmWideStageCost of them (a 10.5% gain measured on the M=512 group),
+    // kGemmWideStageCost of them (a 16-21% gain measured on the Phi-3 groups),
     // but whole tiles balance worse when they are fewer.
     std::vector<mnb::SkTile> seq;
     std::vector<mnb::SkRange> wg;

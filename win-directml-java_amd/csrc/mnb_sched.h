@@ -117,9 +117,11 @@ MNB_HD inline int32_t sk_cf_tile(int32_t MT, int32_t NG, int32_t q) {
 // tile-list order only.
 constexpr int kGemmNTW = 2, kGemmWideNTW = 4;
 constexpr int kGemmFM = 4, kGemmHalfFM = 2, kGemmSkinnyFM = 1;
-// Cost of a 512-column stage in 256-column stages (same-box A/B of the M=512
-// group: 1046 vs 1155 TFLOP/s, so 2 / 1.105).
-constexpr double kGemmWideStageCost = 1.81;
+// Cost of a 512-column stage in 256-column stages (same-box A/B of the
+// Phi-3 groups with the 512-column kernel's current stage order: 256-column
+// against 512-column tiles 947 vs 1103 TFLOP/s at M=128, 1008 vs 1172 at
+// M=256, 1038 vs 1254 at M=512, so 2 x 0.83-0.86).
+constexpr double kGemmWideStageCost = 1.70;
 // One fp32 partial tile of a split 128 x 256 tile (floats).
 constexpr int kSkPartialFloats = 128 * 256;
 // Most workgroups of one GEMM launch: the partial-tile workspace (and the
