@@ -24,11 +24,12 @@
  *     kernel instance shares its command list (MNK:77-81).  Calls that use
  *     them must not overlap: host-memory calls, products with M > 16, products
  *     whose x is staged (fp32 x, x not 16-byte aligned, K not a multiple of
- *     8) and M > 16 groups in stream-K order.  Issue those on one stream or
- *     order them.  The other device-pointer calls (M <= 16 with 16-byte
- *     aligned fp16 x and K a multiple of 8, mnb_group_run of M <= 16 groups
- *     and of M > 16 groups in tile-list order) touch no shared buffer and may
- *     run concurrently on distinct streams.
+ *     8) and M > 16 groups in stream-K order or with parts
+ *     (MNB_ORDER_TILE_LIST_PARTS).  Issue those on one stream or order them.
+ *     The other device-pointer calls (M <= 16 with 16-byte aligned fp16 x
+ *     and K a multiple of 8, mnb_group_run of M <= 16 groups and of M > 16
+ *     groups in plain tile-list order) touch no shared buffer and may run
+ *     concurrently on distinct streams.
  *   - Pointers: by default x/y/out are DEVICE pointers and the call is
  *     asynchronous on `stream` (a hipStream_t; NULL = the context's stream).
  *     With MNB_HOST_MEMORY they are host pointers, the call copies through
@@ -253,7 +254,12 @@ int32_t mnb_max_batch_rows(void);
  * uses the context's GEMM workspace, so it must not overlap other M > 16
  * calls on the context; a group with many tiles (also one of 1 < M <= 16),
  * or whose items have M <= 64 and whose 64-row tiles balance well enough,
- * gives each workgroup whole tiles and uses no workspace.  An item whose x
+ * gives each workgroup whole tiles and uses no workspace, unless a few of
+ * its tiles are much longer than a workgroup's share: those are then cut
+ * along K into parts whose fp32 partial tiles go to the context's GEMM
+ * workspace and are summed by a second launch (MNB_ORDER_TILE_LIST_PARTS,
+ * reported by mnb_group_plan), so such a group run must not overlap other
+ * M > 16 calls on the context either.  An item whose x
  * is 2 GiB or more, or whose packed weight is 4 GiB or more, is refused with
  * MNB_ERR_UNSUPPORTED (mnb_matmul runs such x in row chunks).  The group keeps
  * its own device descriptor table, so mnb_group_run allocates nothing and can
