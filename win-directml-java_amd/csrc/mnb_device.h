@@ -140,8 +140,23 @@ __device__ __forceinline__ const void *uniform_ptr(const void *p) {
 // (scalar base, 32-bit lane offset): lane l writes LDS[m0 + 16 l].  Issued as
 // inline asm, so the compiler neither tracks it nor moves memory accesses
 // across it; the kernel waits for it explicitly.
+//
+// The compiler's hazard recognizer does not look inside inline asm, so it
+// inserts none of the wait states this load needs.  gfx9 requires 1 between
+// an SALU write of M0 and an LDS DMA: the s_nop 0 here provides it (the
+// compiler sets M0 right before the statement).  It also requires 5 between
+// a VALU write of an SGPR and a vector memory instruction that reads it: the
+// scalar base must not come from a v_readfirstlane or from a v_readlane
+// reload of a spilled SGPR within the 5 instructions before this load.  A
+// build of the GEMM without its MFMAs (a timing copy) placed such a reload
+// right before the load, which then read a stale base and faulted on the
+// address.  Padding every load with s_nop 4 instead costs the M = 512 group
+// launch 1% (the tail that issues these loads is issue-bound), so the
+// library's code objects are checked instead: tests/test_code_objects.py
+// disassembles the built library and fails on any direct-to-LDS load within
+// 5 wait states of a VALU write of its base, on every path to it.
 __device__ __forceinline__ void dma16(uint32_t m0, uint32_t off, const void *base) {
-    asm volatile("global_load_lds_dwordx4 %1, %2" ::"{m0}"(m0), "v"(off), "s"(uniform_ptr(base)) : "memory");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"{m0}"(m0), "v"(off), "s"(uniform_ptr(base)) : "memory");
 }
 
 // Load the SPS scales of one row of one tile (SPS * sizeof(ScaleT) bytes,
