@@ -851,6 +851,18 @@ def test_group_with_long_tiles_cut_into_parts_64_row(ctx):
         w.close()
 
 
+def test_group_with_long_tiles_cut_into_parts_fp32_scales_bs128(ctx):
+    """Parts of 64 x 512 tiles with the export format's block size (bs 128,
+    one scale per row and stage) and fp32 scales with zero points: K = 4800
+    (37.5 blocks: the last stage's block is half outside K) and 4864 items
+    cut into parts among short tiles, rows past M, y +=."""
+    specs = [(64, 512, 200000, np.float16, False), (48, 4800, 1000, np.float32, False),
+             (64, 4864, 896, np.float16, False), (40, 4800, 1000, np.float16, True),
+             (64, 512, 150000, np.float32, True)]
+    for w, _, _ in _check_prefill_group(ctx, specs, 3100, bs=128, plan=(GEMM, PARTS, 64, 512), f32_scales=True):
+        w.close()
+
+
 def test_group_with_long_tiles_cut_into_parts_32_row(ctx):
     """32-row tiles (16 < M <= 32) with parts: K = 4864 and 8192 items (38 and
     64 stages) among 1172 two-stage tiles; M = 17 and 24 ragged."""
