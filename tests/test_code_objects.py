@@ -135,7 +135,7 @@ def _disassemble(lib):
 
 @pytest.fixture(scope="module")
 def library_code():
-    lib = mnb_hip.library_path() if hasattr(mnb_hip, "library_path") else mnb_hip.LIB_PATH
+    lib = mnb_hip.library_path()
     if not os.path.exists(lib):
         pytest.skip("library not built: " + lib)
     if not os.path.exists(OBJDUMP):
