@@ -5,7 +5,10 @@
 //     wave count, then one line "NT ST" per item;
 //   closed-form tile list of a single item (mnb::sk_cf_*): the word "closed",
 //     then lines "G MT NG ST", each checked against sk_tile_list of that item;
-//   "grid", "split" and "parts": see check_grid, check_split, check_parts.
+//   "grid", "split" and "parts": see check_grid, check_split, check_parts;
+//   K-sliced plan of single products (mnb::ks_single_plan): the word
+//   "ksplan", then lines "M NT ST scale_f32 has_zp sps", each answered with
+//   "mb ntw est wgs" (mb 0: no supported block).
 // Exits 1 on the first broken invariant; prints balance (and, for the tile
 // list, locality) figures.
 #include <stdio.h>
@@ -314,6 +317,17 @@ static int check_parts() {
     return 0;
 }
 
+static int print_ksplan() {
+    int M, NT, ST, f32, zp, sps;
+    while (scanf("%d %d %d %d %d %d", &M, &NT, &ST, &f32, &zp, &sps) == 6) {
+        const KsPlan p = ks_single_plan(M, NT, ST, f32, zp, sps, 256);
+        if (p.wgs > 0 && (p.wgs != ks_workgroups(M, NT, p.c) || !ks_config_supported(p.c.mb, p.c.ntw, f32, zp, sps)))
+            return fail("ksplan block", p.c.mb, p.c.ntw);
+        printf("%d %d %.3f %lld\n", p.wgs > 0 ? p.c.mb : 0, p.c.ntw, p.est, (long long)p.wgs);
+    }
+    return 0;
+}
+
 int main() {
     char first[32] = {0};
     if (scanf("%31s", first) != 1) return fail("input", 0, 0);
@@ -322,6 +336,7 @@ int main() {
     if (strcmp(first, "grid") == 0) return check_grid();
     if (strcmp(first, "split") == 0) return check_split();
     if (strcmp(first, "parts") == 0) return check_parts();
+    if (strcmp(first, "ksplan") == 0) return print_ksplan();
     const int G = atoi(first);
     if (G < 1) return fail("input", G, 0);
     std::vector<SkItem> items;

@@ -255,3 +255,63 @@ def test_reduce_split_list_matches_the_gemms_partial_tiles(checker):
         lines.append("%d %s" % (G, " ".join("%d %d" % it for it in items)))
     r = subprocess.run([checker], input="split\n" + "\n".join(lines) + "\n", capture_output=True, text=True)
     assert r.returncode == 0 and r.stdout.startswith("ok split cases=%d" % len(lines)), r.stdout
+
+
+def ksplan(checker, queries):
+    """mnb::ks_single_plan for (M, K, N, scale_f32, has_zp, bs) queries:
+    [(mb, ntw, est, workgroups)]."""
+    lines = []
+    for M, K, N, f32, zp, bs in queries:
+        kpad = -(-K // bs) * bs
+        lines.append("%d %d %d %d %d %d" % (M, -(-N // 16), -(-kpad // 128), f32, zp, 128 // bs))
+    r = subprocess.run([checker], input="ksplan\n" + "\n".join(lines) + "\n", capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout
+    out = [tuple(float(v) for v in line.split()) for line in r.stdout.strip().splitlines()]
+    assert len(out) == len(queries)
+    return [(int(a), int(b), c, int(d)) for a, b, c, d in out]
+
+
+def test_k_sliced_blocks_are_the_fastest_measured(checker):
+    """The K-sliced planner's block for single products, against the fastest
+    of its four blocks measured on MI355X with each block forced (fp16
+    scales, bs 32; the Phi-3 and Qwen2.5-0.5B projections at M = 32 to 512 and
+    random shapes; times in us, same box): with 6 or more super-tiles the
+    block comes from the fit with a per-round cost (the Qwen K = 896 rows,
+    where the first model's 32 x 32 blocks measured 17-19% slower), with
+    fewer (K = 512) from the first model."""
+    cases = [  # (M, K, N) -> (mb, ntw)                       fastest measured block (us)
+        ((256, 896, 1152), (2, 4)),     # 32x64 6.09; 32x32 7.44
+        ((512, 896, 1152), (4, 4)),     # 64x64 8.46; 32x32 10.21
+        ((512, 896, 896), (2, 4)),      # 32x64 6.08; 32x32 7.54
+        ((32, 896, 9728), (2, 4)),      # 32x64 6.07; 32x32 7.41
+        ((64, 896, 9728), (4, 4)),      # 64x64 8.44; 32x32 10.39
+        ((32, 3072, 3072), (2, 1)),     # 32x16 6.26
+        ((64, 3072, 3072), (2, 2)),     # 32x32 7.39
+        ((128, 3072, 3072), (2, 4)),    # 32x64 9.75
+        ((32, 3072, 9216), (2, 4)),     # 32x64 10.29
+        ((64, 3072, 9216), (4, 4)),     # 64x64 14.68
+        ((128, 8192, 3072), (2, 4)),    # 32x64 19.12
+        ((137, 4096, 9850), (4, 4)),    # 64x64 34.56; 32x64 41.92
+        ((78, 8192, 7050), (4, 4)),     # 64x64 27.86; 32x64 34.70
+        ((231, 512, 1760), (2, 2)),     # 32x32 4.72; 32x64 5.12 (K = 512: the first model)
+        ((80, 512, 6023), (2, 2)),      # 32x32 5.62; 64x64 7.49 (K = 512: the first model)
+    ]
+    got = ksplan(checker, [(M, K, N, 0, 0, 32) for (M, K, N), _ in cases])
+    for ((M, K, N), want), (mb, ntw, _, wgs) in zip(cases, got):
+        assert (mb, ntw) == want, (M, K, N, (mb, ntw), want)
+        assert wgs == -(-N // (16 * ntw)) * -(-M // (16 * mb))
+
+
+def test_k_sliced_plan_respects_supported_blocks(checker):
+    """Over random shapes and every weight variant the planner returns a
+    block the kernel is compiled for (no 64 x 64 block with bs 16 or with
+    fp32 scales and zero points) and its workgroup count."""
+    rng = np.random.default_rng(41)
+    queries = []
+    for _ in range(3000):
+        queries.append((int(rng.integers(17, 2049)), int(rng.integers(8, 20000)), int(rng.integers(1, 200000)),
+                        int(rng.integers(0, 2)), int(rng.integers(0, 2)), int(rng.choice([16, 32, 64, 128]))))
+    for (M, K, N, f32, zp, bs), (mb, ntw, est, wgs) in zip(queries, ksplan(checker, queries)):
+        assert mb in (2, 4) and est > 0
+        if mb == 4:
+            assert bs != 16 and not (f32 and zp), (M, K, N, f32, zp, bs)

@@ -278,79 +278,6 @@ static hipError_t ks_sps(int sps, const KsConfig &c, dim3 grid, dim3 block, hipS
     }
 }
 
-bool ks_config_supported(int mb, int ntw, int scale_f32, int has_zp, int sps) {
-    if (mb == 2 && (ntw == 1 || ntw == 2 || ntw == 4)) return true;
-    if (mb == 1 && ntw == 4) return true;   // 9 <= M <= 16 (ks_skinny_plan)
-    // 16 output units per wave leave registers for the weights of one
-    // super-tile only where their scales and zero points are small
-    return mb == 4 && ntw == 4 && sps != 8 && !(scale_f32 && has_zp);
-}
-
-int ks_waves(int ST) { return ST < kKsMaxWaves ? ST : kKsMaxWaves; }
-
-// Cost model of one launch, fitted to single-product timings of the Phi-3
-// projections (K 3072 and 8192, N 3072 to 32064, M 17 to 512): a workgroup
-// alone on its CU takes c + k us per super-tile of each wave; with more
-// workgroups than CUs the chip sustains thr wave-super-tiles per us (at 256
-// CUs).  The launch takes the longer of the two.  (Output blocks of 64 x 16,
-// 64 x 32 and 128 x 32 were measured too; with their fitted costs the model
-// never prefers them over 2100 shapes from K 256 to 14336 and N 64 to 151936.)
-//
-// Which block runs, where the model above says this kernel beats the GEMM,
-// comes from a second fit that also charges each round of workgroups a fixed
-// cost r (launch of the round, the LDS reduction, the epilogue): c2 + max(
-// rounds x (super-tiles per wave x k2 + r), the same chip-rate term), fitted
-// to every block forced on the Phi-3 and Qwen2.5-0.5B projections (K 896 to
-// 8192, N 896 to 151936, M 32 to 512; median error 2.6-5% against 6.5-10%
-// for the first model, whose error grows with the rounds).  It is used for
-// products of 6 or more super-tiles (K > 640): on 36 random shapes where the
-// two fits disagree, the second one's blocks ran 5% faster in total (12
-// shapes 13-21% faster, one 2% slower), while on shorter K, where several
-// workgroups share a CU, it misjudged them.  The choice between this kernel
-// and the GEMM stays with the first model.
-struct KsCost {
-    int mb, ntw;
-    double c, k, thr;
-    double c2, k2, r2, thr2;
-};
-static const KsCost kKsCosts[] = {
-    {2, 1, 3.06, 0.88, 2114.0, 2.417, 0.878, 0.687, 2223.1},
-    {2, 2, 2.92, 1.16, 1138.0, 1.346, 1.311, 1.715, 1376.7},
-    {2, 4, 3.86, 1.58, 757.0, 1.177, 1.754, 2.901, 693.6},
-    {4, 4, 5.50, 2.30, 469.0, 0.932, 2.543, 4.603, 422.6},
-};
-constexpr int kKsRoundCostMinST = 6;
-
-KsPlan ks_single_plan(int M, int NT, int ST, int scale_f32, int has_zp, int sps, int cu_count) {
-    KsPlan best{{0, 0}, 0.0, 0};
-    KsConfig block{0, 0};
-    double block_est = 0.0;
-    const int cu = cu_count > 0 ? cu_count : 256;
-    const int W = ks_waves(ST);
-    const double spw = (double)ST / W;
-    for (const KsCost &k : kKsCosts) {
-        if (!ks_config_supported(k.mb, k.ntw, scale_f32, has_zp, sps)) continue;
-        const KsConfig c{k.mb, k.ntw};
-        const int64_t wgs = ks_workgroups(M, NT, c);
-        const double rounds = (double)((wgs + cu - 1) / cu);
-        const double alone = rounds * spw * k.k;
-        const double busy = (double)wgs * W * spw / (k.thr * cu / 256.0);
-        const double est = k.c + std::max(alone, busy);
-        if (best.wgs == 0 || est < best.est) best = KsPlan{c, est, wgs};
-        const double est2 =
-            k.c2 + std::max(rounds * (spw * k.k2 + k.r2), (double)wgs * W * spw / (k.thr2 * cu / 256.0));
-        if (block.mb == 0 || est2 < block_est) {
-            block = c;
-            block_est = est2;
-        }
-    }
-    if (best.wgs > 0 && ST >= kKsRoundCostMinST) {
-        best.c = block;
-        best.wgs = ks_workgroups(M, NT, block);
-    }
-    return best;
-}
-
 // Products with 9 <= M <= 16: the GEMV (one workgroup per n-tile, so every
 // n-tile reads all 16 x rows again) or this kernel with 16 x 64 output blocks
 // (x read once per four n-tiles, each weight tile dequantized once).  Model
@@ -409,9 +336,6 @@ KsPlan ks_skinny_plan(const WeightGeom &g, int32_t M, int32_t cu_count) {
     return est <= kSkinnyMargin * none.est ? KsPlan{c, est, wgs} : none;
 }
 
-int64_t ks_workgroups(int M, int NT, const KsConfig &c) {
-    return (int64_t)((NT + c.ntw - 1) / c.ntw) * ((M + 16 * c.mb - 1) / (16 * c.mb));
-}
 
 hipError_t launch_gemm_ks(const mnb_weight *w, const MatmulArgs &a, const KsConfig &c, hipStream_t stream) {
     const WeightGeom &g = w->g;

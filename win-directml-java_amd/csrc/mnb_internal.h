@@ -255,10 +255,6 @@ hipError_t launch_gemm_group(const GemmGroupPlan &g, float *ws, size_t ws_bytes,
 // products, M > 16): workgroup (m-block, n-group) owns 16 mb rows x 16 ntw
 // columns of y over the whole K; no split tile, no workspace, no second
 // launch.  Rows of x come in chunks of at most 2 GiB (32-bit offsets).
-constexpr int kKsMaxWaves = 8;
-struct KsConfig {
-    int mb, ntw;   // 16-row blocks of x and 16-row n-tiles per workgroup
-};
 struct KsParams {
     const void *q_t;
     const void *s_t;
@@ -270,17 +266,7 @@ struct KsParams {
     int32_t y_f16, accumulate, y_vec;  // y_vec: four-column stores are aligned
     float unfold;                      // 2^-fold_exp of the weight
 };
-bool ks_config_supported(int mb, int ntw, int scale_f32, int has_zp, int sps);
-int ks_waves(int ST);
-int64_t ks_workgroups(int M, int NT, const KsConfig &c);
 hipError_t launch_gemm_ks(const mnb_weight *w, const MatmulArgs &a, const KsConfig &c, hipStream_t stream);
-// The configuration with the smallest estimated time (us) for one product.
-struct KsPlan {
-    KsConfig c;
-    double est;
-    int64_t wgs;
-};
-KsPlan ks_single_plan(int M, int NT, int ST, int scale_f32, int has_zp, int sps, int cu_count);
 // How one product (one chunk of at most 2 GiB of x rows, M > 16) runs: the
 // K-sliced kernel when its cost model expects it to finish before the GEMM's
 // plan, else that plan.

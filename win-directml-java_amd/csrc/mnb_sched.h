@@ -160,6 +160,26 @@ struct SinglePlan {
 };
 SinglePlan sk_single_plan(int M, int NT, int ST, int scale_f32, int sps, int cu_count);
 
+// The K-sliced kernel (one product, M > 16, where the GEMM would have few
+// tiles): workgroup (m-block, n-group) owns 16 mb rows x 16 ntw columns of y
+// over the whole K, its ks_waves(ST) waves on contiguous K slices.
+constexpr int kKsMaxWaves = 8;
+struct KsConfig {
+    int mb, ntw;   // 16-row blocks of x and 16-row n-tiles per workgroup
+};
+bool ks_config_supported(int mb, int ntw, int scale_f32, int has_zp, int sps);
+int ks_waves(int ST);
+int64_t ks_workgroups(int M, int NT, const KsConfig &c);
+// The block this kernel would run one product with and the first cost
+// model's estimate (us) of its best block, which the caller compares with
+// the GEMM's (sk_single_plan).
+struct KsPlan {
+    KsConfig c;
+    double est;
+    int64_t wgs;
+};
+KsPlan ks_single_plan(int M, int NT, int ST, int scale_f32, int has_zp, int sps, int cu_count);
+
 // The split tiles of one launch, passed by value in the reduce kernel's
 // arguments, so nothing is allocated: tile t of item `item` and its
 // contributors first .. last in K order.
