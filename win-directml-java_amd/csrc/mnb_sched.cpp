@@ -262,18 +262,20 @@ int ks_waves(int ST) { return ST < kKsMaxWaves ? ST : kKsMaxWaves; }
 // 64 x 32 and 128 x 32 were measured too; with their fitted costs the model
 // never prefers them over 2100 shapes from K 256 to 14336 and N 64 to 151936.)
 //
-// Which block runs, where the model above says this kernel beats the GEMM,
-// comes from a second fit that also charges each round of workgroups a fixed
-// cost r (launch of the round, the LDS reduction, the epilogue): c2 + max(
-// rounds x (super-tiles per wave x k2 + r), the same chip-rate term), fitted
-// to every block forced on the Phi-3 and Qwen2.5-0.5B projections (K 896 to
-// 8192, N 896 to 151936, M 32 to 512; median error 2.6-5% against 6.5-10%
-// for the first model, whose error grows with the rounds).  It is used for
-// products of 6 or more super-tiles (K > 640): on 36 random shapes where the
-// two fits disagree, the second one's blocks ran 5% faster in total (12
-// shapes 13-21% faster, one 2% slower), while on shorter K, where several
-// workgroups share a CU, it misjudged them.  The choice between this kernel
-// and the GEMM stays with the first model.
+// For products of 6 or more super-tiles (K > 640) the block and the estimate
+// returned (which the caller compares with the GEMM's) come from a second fit
+// that also charges each round of workgroups a fixed cost r (the round's
+// launch, the LDS reduction, the epilogue): c2 + max(rounds x (super-tiles
+// per wave x k2 + r), the same chip-rate term), fitted to every block forced
+// on the Phi-3 and Qwen2.5-0.5B projections (K 896 to 8192, N 896 to 151936,
+// M 32 to 512; median error 2.6-5% against 6.5-10% for the first model,
+// whose error grows with the rounds).  Measured on random shapes where the
+// two fits choose differently: its blocks 5% faster in total (36 shapes, 12
+// of them 13-21% faster, one 2% slower); with its estimate also deciding
+// against the GEMM, 5.2% faster in total (40 shapes: 18 of them 8-31%
+// faster, 8 of them 1-12% slower, where the GEMM's model underestimates its
+// short tiles).  On shorter K, where several workgroups share a CU, it
+// misjudged the blocks, so those keep the first model.
 struct KsCost {
     int mb, ntw;
     double c, k, thr;
@@ -312,6 +314,7 @@ KsPlan ks_single_plan(int M, int NT, int ST, int scale_f32, int has_zp, int sps,
     }
     if (best.wgs > 0 && ST >= kKsRoundCostMinST) {
         best.c = block;
+        best.est = block_est;
         best.wgs = ks_workgroups(M, NT, block);
     }
     return best;

@@ -170,9 +170,9 @@ struct KsConfig {
 bool ks_config_supported(int mb, int ntw, int scale_f32, int has_zp, int sps);
 int ks_waves(int ST);
 int64_t ks_workgroups(int M, int NT, const KsConfig &c);
-// The block this kernel would run one product with and the first cost
-// model's estimate (us) of its best block, which the caller compares with
-// the GEMM's (sk_single_plan).
+// The block this kernel would run one product with and the cost model's
+// estimate (us) for it, which the caller compares with the GEMM's
+// (sk_single_plan).
 struct KsPlan {
     KsConfig c;
     double est;
